@@ -1,0 +1,120 @@
+/*
+ * lbw_attn.h -- C-ABI of liblbw_attn.so: Sage-style quantized DiT attention for MI355X (gfx950).
+ *
+ * Replaces, for the plain self-attention call of the LingBot-World DiT, the native boundary the reference
+ * binds through SageAttention 2.2's pybind functions:
+ *   - lingbot/layers/attention.py:31-36    sageattn(q, k, v, tensor_layout="NHD", ...)
+ *   - lingbot/layers/sage_preq.py:116      per_warp_int8_cuda(q, k, km, BLKQ=128, WARPQ=32, BLKK=64)
+ *   - lingbot/layers/sage_preq.py:121-124  V scale + fp8 V quantisation (_v_scale, _quant_v)
+ *   - lingbot/layers/sage_preq.py:126-127  sm89_compile.qk_int8_sv_f8_accum_f16_fuse_v_scale_attn_inst_buf(...)
+ *   - experiments/modules/sage_kvq.py:78-111  write_chunk / requant_all / attend over a pre-quantised cache
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers owned by the caller; nothing is allocated, freed or synchronised here,
+ *     so every call can be recorded into a HIP graph. `stream` is a hipStream_t (0 = default stream).
+ *   - Sizes and strides are int64 element counts. bf16 tensors are passed as raw 16-bit words.
+ *   - The head dimension is 128 and must be contiguous (stride 1).
+ *   - Return value: LBW_OK (0) or one of the LBW_E* codes below; lbw_status_string() names it.
+ *
+ * Quantised ring cache (one per layer; `layers` of them back to back, slot capacity `cap` tokens, a multiple
+ * of 64; BH = batch * heads; nb = cap / 64):
+ *   k8      int8  [layers][slots][BH][cap][128]       K - mean, per 64-token block int8
+ *   k_scale fp32  [layers][slots][BH][nb]             amax / 127 of each 64-token block
+ *   km      fp32  [layers][slots][BH][128]            per-(head, channel) chunk mean (a bf16 value)
+ *   v8      uint8 [layers][slots][BH][nb][128][64]    e4m3 V, per 64-key block: [channel][position]
+ *   v_scale fp32  [layers][slots][BH][128]            amax / 448 per (head, channel)
+ * Position p of a 64-key V block holds key 32*((p&31)>>4) + 8*((p>>2)&3) + 4*(p>>5) + (p&3).
+ *
+ * Quantised Q (per call): q8 int8 [BH][Lp][128], q_scale fp32 [BH][Lp/32], Lp = Lq rounded up to 128;
+ * bias fp32 [n_seg][BH][Lp] holds q . km of each attended chunk (only read when n_seg > 1).
+ */
+#ifndef LBW_ATTN_H
+#define LBW_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LBW_OK = 0,
+  LBW_E_NULL = 1,        /* a required pointer is null */
+  LBW_E_SHAPE = 2,       /* a size is out of range or inconsistent */
+  LBW_E_ALIGN = 3,       /* a pointer or stride breaks the 16-byte alignment the kernels load with */
+  LBW_E_DEVICE = 4,      /* the current device is not gfx950 */
+  LBW_E_LAUNCH = 5,      /* the kernel launch failed */
+  LBW_E_SEGMENTS = 6     /* the attended-chunk table is invalid */
+};
+
+#define LBW_HEAD_DIM 128
+#define LBW_MAX_SEGMENTS 8
+
+/* Name of a status code. */
+const char* lbw_status_string(int status);
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int lbw_version(void);
+
+/* Bytes of scratch `lbw_kv_requant` needs for `layers` chunks of `len` tokens and `bh` batch*heads. */
+int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len);
+
+/*
+ * Quantise bf16 K and V chunks of `len` tokens into slot `slot` of `layers` consecutive layer caches:
+ * the per-(head, channel) K mean, K - mean as int8 per 64-token block, V as e4m3 with one scale per
+ * (head, channel). Replaces sage_kvq.requant_all + write_chunk (experiments/modules/sage_kvq.py:78-98)
+ * and Sage's per_warp_int8 K part / per_channel_fp8 (lingbot/layers/sage_preq.py:115-124).
+ * k/v element (layer l, batch b, token t, head h, channel d) sits at l*s_layer + b*s_batch + t*s_tok
+ * + h*s_head + d. `workspace` holds lbw_kv_requant_workspace_bytes() bytes, 16-byte aligned; its
+ * contents need not be preserved between calls. Tokens in [len, ceil64(len)) of the slot are written
+ * as zero; blocks past ceil64(len) are left untouched (the attention never reads them).
+ */
+int lbw_kv_requant(const uint16_t* k, const uint16_t* v,
+                   int64_t layers, int64_t batch, int64_t len, int64_t heads,
+                   int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok, int64_t k_s_head,
+                   int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
+                   int8_t* k8, float* k_scale, float* km, uint8_t* v8, float* v_scale,
+                   int64_t slots, int64_t cap, int64_t slot,
+                   void* workspace, void* stream);
+
+/*
+ * Quantise bf16 Q [batch][lq][heads][128] (strides s_batch, s_tok, s_head) to int8 with one scale per
+ * 32 rows (Sage per_warp_int8 Q part with BLKQ=128, WARPQ=32: lingbot/layers/sage_preq.py:116,
+ * experiments/modules/sage_kvq.py:104). When n_seg > 1 it also writes bias[c][bh][row] = q . km of chunk
+ * seg_slot[c] of the (layer-offset) cache `km` with `slots` slots. seg_slot is a host array.
+ */
+int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
+                int64_t s_batch, int64_t s_tok, int64_t s_head,
+                int8_t* q8, float* q_scale,
+                const float* km, int64_t slots, int n_seg, const int32_t* seg_slot, float* bias,
+                void* stream);
+
+/*
+ * Quantized attention of Q (from lbw_quant_q) over the chunks seg_slot[0..n_seg) of one layer's cache
+ * (pointers already offset to that layer), chunk c holding seg_len[c] valid tokens (1..cap). Writes bf16
+ * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the
+ * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA, fp32 accumulation, V scale
+ * and 1 / row sum applied at the end. Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
+ * 126-127; experiments/modules/sage_kvq.py:107-110). seg_slot / seg_len are host arrays.
+ */
+int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias,
+                 int64_t batch, int64_t lq, int64_t heads,
+                 const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* v_scale,
+                 int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
+                 uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
+                 float sm_scale, void* stream);
+
+/*
+ * Debug: int32 logits S[bh][i][j] = sum_d q8[bh][i][d] * k8[slot][bh][j][d] for i < Lp and j < cap, through
+ * the same LDS tiles and int8 MFMA as lbw_attn_fwd. out is int32 [BH][Lp][cap]. Has no reference
+ * counterpart; it exists to check the QK^T product bit for bit.
+ */
+int lbw_qk_logits_i32(const int8_t* q8, int64_t bh, int64_t lq,
+                      const int8_t* k8, int64_t slots, int64_t cap, int64_t slot,
+                      int32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LBW_ATTN_H */

@@ -1,0 +1,227 @@
+// K/V re-quant of finished chunks into the quantised ring cache (gfx950).
+//
+// Three launches, all over (64-token block, batch*head, layer):
+//   1. kv_stats:    per block, fp32 column sums of K and column max |V| (read K and V once).
+//   2. kv_finalize: per (layer, bh, channel), sum the block sums left to right, mean -> bf16, V scale.
+//   3. kv_quant:    K - mean -> int8 per 64-token block; V * (448 / amax) -> e4m3 in the permuted block
+//                   layout (read K and V a second time; a layer's 37 MB is normally still in the MALL).
+// The column-sum order is fixed (see the oracle's chunk_mean): s = x[rg] + x[rg+16] + x[rg+32] + x[rg+48]
+// per thread, then rg = 0..15 left to right per block, then the blocks left to right, so the mean is the
+// same bits on every run and on the CPU.
+#include "lbw_common.h"
+
+namespace lbw {
+
+struct ReqArgs {
+  int64_t len, heads, bh, slots, cap, slot, nb, nbc;  // nb: blocks of len, nbc: blocks of cap
+  int64_t k_sl, k_sb, k_st, k_sh;
+  int64_t v_sl, v_sb, v_st, v_sh;
+};
+
+__global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restrict__ k,
+                                                       const uint16_t* __restrict__ v, ReqArgs a,
+                                                       float* __restrict__ part_sum,
+                                                       float* __restrict__ part_amax) {
+  __shared__ float s_sum[16][D];
+  __shared__ float s_max[16][D];
+  const int blk = blockIdx.x, bh = blockIdx.y, layer = blockIdx.z;
+  const int t = threadIdx.x, cg = t & 15, rg = t >> 4;
+  const int64_t b = bh / a.heads, h = bh % a.heads;
+  const uint16_t* kp = k + layer * a.k_sl + b * a.k_sb + h * a.k_sh + cg * 8;
+  const uint16_t* vp = v + layer * a.v_sl + b * a.v_sb + h * a.v_sh + cg * 8;
+  float s[8], m[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) { s[c] = 0.f; m[c] = 0.f; }
+  v4i kw[4], vw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t tok = (int64_t)blk * KB + rg + 16 * i;
+    if (tok < a.len) {
+      kw[i] = *(const v4i*)(kp + tok * a.k_st);
+      vw[i] = *(const v4i*)(vp + tok * a.v_st);
+    } else {
+      kw[i] = v4i{0, 0, 0, 0};
+      vw[i] = v4i{0, 0, 0, 0};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float kf[8], vf[8];
+    unpack8(kw[i], kf);
+    unpack8(vw[i], vf);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      s[c] = __fadd_rn(s[c], kf[c]);
+      m[c] = fmaxf(m[c], fabsf(vf[c]));
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    s_sum[rg][cg * 8 + c] = s[c];
+    s_max[rg][cg * 8 + c] = m[c];
+  }
+  __syncthreads();
+  if (t < D) {
+    float acc = 0.f, mx = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc = __fadd_rn(acc, s_sum[r][t]);
+      mx = fmaxf(mx, s_max[r][t]);
+    }
+    const int64_t o = (((int64_t)layer * a.bh + bh) * a.nb + blk) * D + t;
+    part_sum[o] = acc;
+    part_amax[o] = mx;
+  }
+}
+
+__global__ __launch_bounds__(128) void kv_finalize_kernel(ReqArgs a, const float* __restrict__ part_sum,
+                                                          const float* __restrict__ part_amax,
+                                                          float* __restrict__ v_recip,
+                                                          float* __restrict__ km,
+                                                          float* __restrict__ v_scale) {
+  const int bh = blockIdx.x, layer = blockIdx.y, c = threadIdx.x;
+  const int64_t base = ((int64_t)layer * a.bh + bh) * a.nb * D + c;
+  float tot = 0.f, mx = 0.f;
+  for (int64_t b = 0; b < a.nb; ++b) {
+    tot = __fadd_rn(tot, part_sum[base + b * D]);
+    mx = fmaxf(mx, part_amax[base + b * D]);
+  }
+  const float mean = __fdiv_rn(tot, (float)a.len);
+  mx = fmaxf(mx, AMAX_FLOOR);
+  const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + c;
+  km[so] = bf16_round(mean);
+  v_scale[so] = __fdiv_rn(mx, V_MAX);
+  v_recip[((int64_t)layer * a.bh + bh) * D + c] = __fdiv_rn(V_MAX, mx);
+}
+
+// Thread t owns channels 8*(t & 15) .. +8 and the 4 consecutive keys 4*(t >> 4) .. +4 of the block, so its
+// e4m3 V bytes for one channel are 4 adjacent positions (one dword) of the permuted layout.
+__global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restrict__ k,
+                                                       const uint16_t* __restrict__ v, ReqArgs a,
+                                                       const float* __restrict__ v_recip,
+                                                       int8_t* __restrict__ k8, float* __restrict__ k_scale,
+                                                       const float* __restrict__ km,
+                                                       uint8_t* __restrict__ v8) {
+  __shared__ uint32_t s_v[D * 16];   // [channel][16 dwords], dword index xor-swizzled by channel >> 3
+  __shared__ float s_red[4];
+  const int blk = blockIdx.x, bh = blockIdx.y, layer = blockIdx.z;
+  const int t = threadIdx.x, cg = t & 15, kq = t >> 4;
+  const int64_t b = bh / a.heads, h = bh % a.heads;
+  const uint16_t* kp = k + layer * a.k_sl + b * a.k_sb + h * a.k_sh + cg * 8;
+  const uint16_t* vp = v + layer * a.v_sl + b * a.v_sb + h * a.v_sh + cg * 8;
+  const int64_t slot_bh = ((int64_t)layer * a.slots + a.slot) * a.bh + bh;
+  float mean[8], vrec[8];
+  {
+    const float* kmp = km + slot_bh * D + cg * 8;
+    const float* vrp = v_recip + ((int64_t)layer * a.bh + bh) * D + cg * 8;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) { mean[c] = kmp[c]; vrec[c] = vrp[c]; }
+  }
+  float x[4][8];
+  uint32_t vb[8];   // per channel: 4 e4m3 bytes of keys 4kq .. 4kq+3
+#pragma unroll
+  for (int c = 0; c < 8; ++c) vb[c] = 0;
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t tok = (int64_t)blk * KB + kq * 4 + j;
+    const bool ok = tok < a.len;
+    v4i kw = ok ? *(const v4i*)(kp + tok * a.k_st) : v4i{0, 0, 0, 0};
+    v4i vw = ok ? *(const v4i*)(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
+    float kf[8], vf[8];
+    unpack8(kw, kf);
+    unpack8(vw, vf);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      x[j][c] = ok ? __fsub_rn(kf[c], mean[c]) : 0.f;
+      amax = fmaxf(amax, fabsf(x[j][c]));
+    }
+#pragma unroll
+    for (int c = 0; c < 8; c += 2) {
+      float y0 = fminf(fmaxf(__fmul_rn(vf[c], vrec[c]), -V_MAX), V_MAX);
+      float y1 = fminf(fmaxf(__fmul_rn(vf[c + 1], vrec[c + 1]), -V_MAX), V_MAX);
+      const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+      vb[c] |= (pk & 0xFFu) << (8 * j);
+      vb[c + 1] |= ((pk >> 8) & 0xFFu) << (8 * j);
+    }
+  }
+  // block amax over 64 tokens x 128 channels
+  amax = wave_max(amax);
+  if ((t & 63) == 0) s_red[t >> 6] = amax;
+  // e4m3 V dwords into the transposed tile: row = channel, dword = position / 4
+  const int pdw = v_pos_of_key(kq * 4) >> 2;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int ch = cg * 8 + c;
+    s_v[ch * 16 + (pdw ^ (ch >> 3))] = vb[c];
+  }
+  __syncthreads();
+  amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  amax = fmaxf(amax, AMAX_FLOOR);
+  const float recip = __fdiv_rn(127.f, amax);
+  if (t == 0) k_scale[slot_bh * a.nbc + blk] = __fdiv_rn(amax, 127.f);
+  int8_t* kout = k8 + (slot_bh * a.cap + (int64_t)blk * KB) * D + cg * 8;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      lo |= ((uint32_t)quant_i8(x[j][c], recip) & 0xFFu) << (8 * c);
+      hi |= ((uint32_t)quant_i8(x[j][c + 4], recip) & 0xFFu) << (8 * c);
+    }
+    *(uint2*)(kout + (kq * 4 + j) * D) = make_uint2(lo, hi);
+  }
+  // V tile out: thread t writes 32 contiguous bytes (channel t >> 1, positions 32 * (t & 1) ..)
+  {
+    const int ch = t >> 1, d0 = (t & 1) * 8;
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = s_v[ch * 16 + ((d0 + i) ^ (ch >> 3))];
+    uint8_t* vout = v8 + (slot_bh * a.nbc + blk) * (D * KB) + ch * KB + d0 * 4;
+    *(v4i*)vout = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    *(v4i*)(vout + 16) = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+  }
+}
+
+}  // namespace lbw
+
+using namespace lbw;
+
+extern "C" int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len) {
+  if (layers <= 0 || bh <= 0 || len <= 0) return 0;
+  const int64_t nb = (len + KB - 1) / KB;
+  return (2 * layers * bh * nb * D + layers * bh * D) * (int64_t)sizeof(float);
+}
+
+extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
+                              int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch,
+                              int64_t k_s_tok, int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch,
+                              int64_t v_s_tok, int64_t v_s_head, int8_t* k8, float* k_scale, float* km,
+                              uint8_t* v8, float* v_scale, int64_t slots, int64_t cap, int64_t slot,
+                              void* workspace, void* stream) {
+  if (!k || !v || !k8 || !k_scale || !km || !v8 || !v_scale || !workspace) return LBW_E_NULL;
+  if (layers <= 0 || batch <= 0 || heads <= 0 || len <= 0 || slots <= 0 || cap <= 0) return LBW_E_SHAPE;
+  if (cap % KB != 0 || len > cap || slot < 0 || slot >= slots) return LBW_E_SHAPE;
+  if (layers > 65535 || batch * heads > 65535 || cap / KB > (int64_t)1 << 30) return LBW_E_SHAPE;
+  const int64_t strides[8] = {k_s_layer, k_s_batch, k_s_tok, k_s_head, v_s_layer, v_s_batch, v_s_tok, v_s_head};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return LBW_E_ALIGN;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)workspace) & 15) return LBW_E_ALIGN;
+  ReqArgs a;
+  a.len = len; a.heads = heads; a.bh = batch * heads; a.slots = slots; a.cap = cap; a.slot = slot;
+  a.nb = (len + KB - 1) / KB;
+  a.nbc = cap / KB;
+  a.k_sl = k_s_layer; a.k_sb = k_s_batch; a.k_st = k_s_tok; a.k_sh = k_s_head;
+  a.v_sl = v_s_layer; a.v_sb = v_s_batch; a.v_st = v_s_tok; a.v_sh = v_s_head;
+  float* part_sum = (float*)workspace;
+  float* part_amax = part_sum + layers * a.bh * a.nb * D;
+  float* v_recip = part_amax + layers * a.bh * a.nb * D;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
+  hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
+  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers), dim3(128), 0, st, a,
+                     part_sum, part_amax, v_recip, km, v_scale);
+  hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8);
+  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
+  return LBW_OK;
+}

@@ -1,0 +1,69 @@
+// Shared device helpers of the gfx950 quantized attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lbw_attn.h"
+
+namespace lbw {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int D = LBW_HEAD_DIM;   // head dim
+constexpr int KB = 64;            // keys per K scale block / V block
+constexpr int QG = 32;            // query rows per Q scale
+constexpr int QT = 128;           // query rows per tile (Lq padding)
+constexpr float V_MAX = 448.f;
+constexpr float AMAX_FLOOR = 1e-7f;
+constexpr float P_OFFSET = 8.807f;           // log2(448): P = exp2(s - m + P_OFFSET) <= 448
+constexpr int S_MAGIC = 0x4B400000;          // int bits of 12582912.0f = 1.5 * 2^23
+constexpr float S_MAGIC_F = 12582912.f;      // float(S_MAGIC + s) == 12582912 + s for |s| < 2^22
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// fp32 -> nearest bf16 (ties to even) as fp32; finite inputs.
+__device__ __forceinline__ float bf16_round(float x) {
+  uint32_t u = __float_as_uint(x);
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  return __uint_as_float(u);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  u = u + 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Unpack 8 bf16 held in a 16-byte vector to fp32.
+__device__ __forceinline__ void unpack8(const v4i w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t u = (uint32_t)w[i];
+    f[2 * i] = __uint_as_float(u << 16);
+    f[2 * i + 1] = __uint_as_float(u & 0xFFFF0000u);
+  }
+}
+
+// round(x * recip) to int8 with saturation; explicit roundings so no FMA contraction can occur.
+__device__ __forceinline__ int quant_i8(float x, float recip) {
+  float r = rintf(__fmul_rn(x, recip));
+  r = fminf(fmaxf(r, -128.f), 127.f);
+  return (int)r;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+// Position of key k (0..63) inside a 64-key fp8 V block.
+__device__ __forceinline__ int v_pos_of_key(int k) {
+  return 32 * ((k >> 2) & 1) + 16 * ((k >> 5) & 1) + 4 * ((k >> 3) & 3) + (k & 3);
+}
+
+}  // namespace lbw

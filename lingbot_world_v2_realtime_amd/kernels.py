@@ -1,0 +1,161 @@
+"""Thin torch-side wrappers over the C-ABI: device memory and the current stream come from torch, the work is
+done by the HIP kernels in liblbw_attn.so. Nothing here computes on the CPU."""
+import ctypes
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+K_BLOCK = 64
+Q_TILE = 128
+Q_GROUP = 32
+MAX_SEGMENTS = 8
+ctypes_i32 = ctypes.c_int32
+
+
+def pad_to(n, m):
+    return (n + m - 1) // m * m
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _require_cuda_bf16(name, t):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor (the quantized path has no CPU implementation)")
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+        raise ValueError(f"{name} must have a contiguous head dim of {HEAD_DIM}, got shape {tuple(t.shape)}")
+
+
+class RingCache:
+    """Quantised K/V ring for `layers` layers x `slots` chunk slots of capacity `cap` tokens (a multiple of 64).
+
+    Device layout (include/lbw_attn.h): k8 int8 [L, S, BH, cap, 128]; k_scale fp32 [L, S, BH, cap/64];
+    km fp32 [L, S, BH, 128]; v8 uint8 [L, S, BH, cap/64, 128, 64]; v_scale fp32 [L, S, BH, 128].
+    """
+
+    def __init__(self, layers, batch, heads, cap, slots, device):
+        if cap % K_BLOCK:
+            raise ValueError("cap must be a multiple of 64")
+        self.layers, self.batch, self.heads, self.cap, self.slots = layers, batch, heads, cap, slots
+        bh, nb = batch * heads, cap // K_BLOCK
+        dev = torch.device(device)
+        self.k8 = torch.zeros(layers, slots, bh, cap, HEAD_DIM, dtype=torch.int8, device=dev)
+        self.k_scale = torch.zeros(layers, slots, bh, nb, dtype=torch.float32, device=dev)
+        self.km = torch.zeros(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
+        self.v8 = torch.zeros(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev)
+        self.v_scale = torch.ones(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
+        self.device = dev
+
+    @property
+    def bh(self):
+        return self.batch * self.heads
+
+    def layer_view(self, layer):
+        """(k8, k_scale, km, v8, v_scale) of one layer, for the per-layer entry points."""
+        return (self.k8[layer], self.k_scale[layer], self.km[layer], self.v8[layer], self.v_scale[layer])
+
+
+def requant_workspace(layers, bh, length, device):
+    nbytes = _lib.load().lbw_kv_requant_workspace_bytes(layers, bh, length)
+    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def kv_requant(k, v, ring, slot, layer0=0, workspace=None):
+    """Quantise bf16 K, V chunks into `slot` of `ring`.
+
+    k, v: [B, L, H, 128] (one layer; written to layer `layer0`) or [layers, B, L, H, 128] (layers
+    layer0 .. layer0 + layers - 1), any strides with a contiguous head dim.
+    """
+    lib = _lib.load()
+    _require_cuda_bf16("k", k)
+    _require_cuda_bf16("v", v)
+    if k.shape != v.shape:
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    if k.dim() == 4:
+        k, v = k.unsqueeze(0), v.unsqueeze(0)
+    nl, b, n, h, _ = k.shape
+    if b != ring.batch or h != ring.heads or n > ring.cap or layer0 + nl > ring.layers:
+        raise ValueError(f"chunk {tuple(k.shape)} does not fit the ring "
+                         f"(layers {ring.layers}, batch {ring.batch}, heads {ring.heads}, cap {ring.cap})")
+    if workspace is None:
+        workspace = requant_workspace(nl, b * h, n, k.device)
+    ks, vs = k.stride(), v.stride()
+    st = lib.lbw_kv_requant(
+        _ptr(k), _ptr(v), nl, b, n, h, ks[0], ks[1], ks[2], ks[3], vs[0], vs[1], vs[2], vs[3],
+        _ptr(ring.k8[layer0]), _ptr(ring.k_scale[layer0]), _ptr(ring.km[layer0]), _ptr(ring.v8[layer0]),
+        _ptr(ring.v_scale[layer0]), ring.slots, ring.cap, slot, _ptr(workspace), _stream(k))
+    _lib.check(st, "lbw_kv_requant")
+
+
+def quant_q(q, layout="NHD", ring=None, layer=0, seg_slots=()):
+    """bf16 Q -> (q8 [BH, Lp, 128], q_scale [BH, Lp/32], bias [n_seg, BH, Lp] or None)."""
+    lib = _lib.load()
+    _require_cuda_bf16("q", q)
+    b, lq, h, s_b, s_t, s_h = _dims(q, layout)
+    bh, lp = b * h, pad_to(lq, Q_TILE)
+    q8 = torch.empty(bh, lp, HEAD_DIM, dtype=torch.int8, device=q.device)
+    qs = torch.empty(bh, lp // Q_GROUP, dtype=torch.float32, device=q.device)
+    n_seg = len(seg_slots)
+    bias = None
+    km_ptr, slots, seg_arr = None, 1, None
+    if n_seg > 1:
+        bias = torch.empty(n_seg, bh, lp, dtype=torch.float32, device=q.device)
+        km_ptr, slots = _ptr(ring.km[layer]), ring.slots
+        seg_arr = (ctypes_i32 * n_seg)(*seg_slots)
+    st = lib.lbw_quant_q(_ptr(q), b, lq, h, s_b, s_t, s_h, _ptr(q8), _ptr(qs), km_ptr, slots, n_seg,
+                         seg_arr, _ptr(bias), _stream(q))
+    _lib.check(st, "lbw_quant_q")
+    return q8, qs, bias
+
+
+def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_lens, out, layout="NHD",
+             sm_scale=None):
+    """Quantized attention of quantised Q over the chunks `seg_slots` (with `seg_lens` valid tokens) of one
+    layer of `ring`, written into bf16 `out` ([B, Lq, H, 128] NHD or [B, H, Lq, 128] HND)."""
+    lib = _lib.load()
+    n_seg = len(seg_slots)
+    if not 1 <= n_seg <= MAX_SEGMENTS or len(seg_lens) != n_seg:
+        raise ValueError(f"need 1..{MAX_SEGMENTS} chunks with a length each, got {seg_slots} / {seg_lens}")
+    _, _, _, o_b, o_t, o_h = _dims(out, layout)
+    sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
+    k8, ksc, _, v8, vsc = ring.layer_view(layer)
+    slot_arr = (ctypes_i32 * n_seg)(*seg_slots)
+    len_arr = (ctypes_i32 * n_seg)(*seg_lens)
+    st = lib.lbw_attn_fwd(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
+                          _ptr(v8), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr, _ptr(out),
+                          o_b, o_t, o_h, sm_scale, _stream(q8))
+    _lib.check(st, "lbw_attn_fwd")
+    return out
+
+
+def qk_logits(q8, lq, ring, layer, slot):
+    """Debug: int32 S [BH, Lp, cap] of quantised Q against one slot, via the attention's MFMA tiles."""
+    lib = _lib.load()
+    bh, lp = q8.shape[0], q8.shape[1]
+    out = torch.empty(bh, lp, ring.cap, dtype=torch.int32, device=q8.device)
+    st = lib.lbw_qk_logits_i32(_ptr(q8), bh, lq, _ptr(ring.k8[layer]), ring.slots, ring.cap, slot, _ptr(out),
+                               _stream(q8))
+    _lib.check(st, "lbw_qk_logits_i32")
+    return out
+
+
+def _dims(x, layout):
+    """(B, L, H, stride_batch, stride_tok, stride_head) of an NHD [B, L, H, D] or HND [B, H, L, D] tensor."""
+    if x.dim() != 4:
+        raise ValueError(f"expected a 4-d tensor, got shape {tuple(x.shape)}")
+    s = x.stride()
+    if layout == "NHD":
+        return x.shape[0], x.shape[1], x.shape[2], s[0], s[1], s[2]
+    if layout == "HND":
+        return x.shape[0], x.shape[2], x.shape[1], s[0], s[2], s[1]
+    raise ValueError(f"tensor_layout must be 'NHD' or 'HND', got {layout!r}")
+

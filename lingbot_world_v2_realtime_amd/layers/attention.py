@@ -1,0 +1,80 @@
+"""Attention backends of the DiT, with the quantized MI355X kernels in place of SageAttention 2.2.
+
+Mirrors lingbot/layers/attention.py:1-40. `LINGBOT_ATTN=sage` (read at import time, as the reference does
+at :22-24) routes the plain batched self-attention call -- no q_lens / k_lens, no dropout, non-causal, the
+only way the causal DiT calls it -- through `sage_attention`: INT8 QK^T and FP8 PV in HIP kernels on gfx950.
+Everything else goes to the paper's attention semantics (reference/wan/modules/attention.py:132-178), served
+here by PyTorch SDPA because flash_attn has no ROCm wheel in this stack.
+"""
+import os
+import warnings
+
+import torch
+
+from .. import kernels
+
+__all__ = ["attention", "flash_attention", "sage_attention"]
+
+_QUANT = os.environ.get("LINGBOT_ATTN") in ("sage", "sage_kvq")
+
+
+def sage_attention(q, k, v, tensor_layout="NHD", is_causal=False, sm_scale=None):
+    """Quantized attention, the call `sageattn(q, k, v, tensor_layout, is_causal, sm_scale)` makes on sm_120
+    (per-warp int8 Q, mean-smoothed per-block int8 K, per-channel fp8 V; lingbot/layers/attention.py:34-35).
+
+    q [B, Lq, H, 128], k/v [B, Lk, H, 128] for "NHD" ([B, H, L, 128] for "HND"), bf16 on the GPU. Returns
+    bf16 in q's layout. The K mean and V scales are taken over all Lk keys (one chunk), so the logits need
+    no per-chunk bias. Raises if liblbw_attn.so is missing: there is no fallback.
+    """
+    if is_causal:
+        raise NotImplementedError("the quantized kernel is non-causal; the DiT never calls it causally")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        kernels._require_cuda_bf16(name, t)
+    b, lq, h, *_ = kernels._dims(q, tensor_layout)
+    bk, lk, hk, *_ = kernels._dims(k, tensor_layout)
+    if (bk, hk) != (b, h) or tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
+    if tensor_layout == "HND":
+        k, v = k.transpose(1, 2), v.transpose(1, 2)
+    ring = kernels.RingCache(1, b, h, kernels.pad_to(lk, kernels.K_BLOCK), 1, q.device)
+    kernels.kv_requant(k, v, ring, 0)
+    q8, qs, _ = kernels.quant_q(q, tensor_layout)
+    out = torch.empty_like(q)
+    return kernels.attn_fwd(q8, qs, None, b, lq, h, ring, 0, [0], [lk], out, tensor_layout, sm_scale)
+
+
+def _paper_attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=None, q_scale=None,
+                     causal=False, window_size=(-1, -1), deterministic=False, dtype=torch.bfloat16,
+                     fa_version=None):
+    """The paper's attention when flash_attn is absent: SDPA on [B, L, H, D] inputs
+    (reference/wan/modules/attention.py:163-178; padding masks are ignored there too)."""
+    if q_lens is not None or k_lens is not None:
+        warnings.warn("Padding mask is disabled when using scaled_dot_product_attention. It can have a "
+                      "significant impact on performance.")
+    if q_scale is not None:
+        q = q * q_scale
+    qt, kt, vt = (x.transpose(1, 2).to(dtype) for x in (q, k, v))
+    out = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=None, is_causal=causal,
+                                                           dropout_p=dropout_p, scale=softmax_scale)
+    return out.transpose(1, 2).contiguous()
+
+
+def flash_attention(q, k, v, k_lens=None, **kw):
+    """The paper's FlashAttention call (lingbot/layers/attention.py:16-20); SDPA on this stack."""
+    return _paper_attention(q, k, v, k_lens=k_lens, **kw)
+
+
+def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=None, q_scale=None,
+              causal=False, window_size=(-1, -1), deterministic=False, dtype=None, fa_version=None):
+    """Drop-in for lingbot/layers/attention.py:27-40: same arguments, same routing, q.dtype out."""
+    dtype = torch.bfloat16 if dtype is None else dtype
+    if _QUANT and q_lens is None and k_lens is None and dropout_p == 0. and not causal:
+        out_dtype = q.dtype
+        # the kernels quantise from bf16, whatever compute dtype the caller names
+        x = sage_attention(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16),
+                           tensor_layout="NHD", is_causal=causal, sm_scale=softmax_scale)
+        return x.to(out_dtype)
+    return _paper_attention(q, k, v, q_lens=q_lens, k_lens=k_lens, dropout_p=dropout_p,
+                            softmax_scale=softmax_scale, q_scale=q_scale, causal=causal,
+                            window_size=window_size, deterministic=deterministic, dtype=dtype,
+                            fa_version=fa_version)

@@ -1,0 +1,344 @@
+"""Pure-torch CPU emulation of the quantized attention scheme (the oracle; test infrastructure only).
+
+This restates, on the CPU, the arithmetic the HIP kernels implement, so that the int8 Q/K tensors, every
+scale, the K smoothing mean, the fp8 V bytes and the int32 QK^T logits can be compared bit for bit, and the
+attention output within tolerance. It follows the reference's own pure-torch restatement of SageAttention's
+quantisers and its documentation of the fused kernel:
+
+- Q: int8 per 32-row group of 128-row tiles, scale = amax / 127, amax floored at 1e-7, values
+  x * (127 / amax) in fp32, round half to even, saturate; rows past Lq count as zero
+  (experiments/modules/sage_kvq.py:57-66, :104; rounding statement :14-19).
+- K: subtract the per-(head, channel) mean over the chunk, rounded to bf16 as `k.mean(dim=1)` on a bf16
+  tensor is (lingbot/layers/sage_preq.py:115; sage_kvq.py:85, :96), then int8 per 64-token block as above;
+  tokens past the chunk count as zero after the subtraction (sage_kvq.py:61-63).
+- V: fp8 e4m3 with one scale per (head, channel) (sage_kvq.py:69-75; sage_preq.py:47-78). The reference maps
+  amax to 2.25 because its PV accumulates in fp16 (sage_kvq.py:30-31); the MFMA here accumulates in fp32,
+  so amax maps to the full e4m3 range 448. Values are clamped first because torch's fp32 -> e4m3 cast is
+  round-to-nearest-even but not saturating.
+- Logits: S = q8 . k8 in int32 (experiments/bench_attn/h2_tiles/README.md:45), dequantised with
+  q_scale * k_scale * sm_scale * log2(e) into the exp2 domain; P = exp2(s - m + 8.807) <= 448 cast to e4m3
+  (experiments/bench_attn/phi_calib.md:11-16); O = sum P V / sum P, times the V scale
+  (h2_tiles/README.md:13-20; experiments/bench_attn/splitkv/README.md:62-63).
+- Memory chunks keep their own mean and V scale; the bias q . mean_c of chunk c is added to its logits
+  (a constant per (query, chunk), so it drops out when there is only one chunk).
+
+Order of the K mean (fixed so it is reproducible bit for bit): token t of a chunk sits in 64-token block
+b = t // 64 at row r = t % 64 = rg + 16 * i (rg in 0..15, i in 0..3). In fp32, starting from +0:
+  s[b, rg] = (((0 + x[rg]) + x[rg + 16]) + x[rg + 32]) + x[rg + 48]
+  B[b]     = s[b, 0] + s[b, 1] + ... + s[b, 15]        (left to right)
+  total    = B[0] + B[1] + ... + B[nb - 1]              (left to right)
+  mean     = total / n (fp32, correctly rounded), km = bf16(mean) round to nearest even.
+Padding tokens past n add +0.
+
+fp8 V layout per 64-key block: [channel][64 positions]; position p holds key
+  key(p) = 32 * ((p & 31) >> 4) + 8 * ((p >> 2) & 3) + 4 * (p >> 5) + (p & 3),
+the order in which an MFMA 32x32 int32 output tile of S^T (two tiles per 64 keys) leaves the keys in the
+lanes that then feed P^T to the fp8 PV MFMA, so P needs no reordering between the two products.
+"""
+import numpy as np
+import torch
+
+Q_GROUP = 32            # query rows per Q scale
+Q_TILE = 128            # Lq is padded to whole tiles of this many rows
+K_BLOCK = 64            # keys per K scale and per V block
+HEAD_DIM = 128
+V_MAX = 448.0           # e4m3 max; the V scale maps amax to it
+AMAX_FLOOR = 1e-7
+P_OFFSET = 8.807        # log2(448): P = exp2(s - m + P_OFFSET) <= 448
+LOG2E = 1.4426950408889634
+
+
+def pad_to(n, m):
+    return (n + m - 1) // m * m
+
+
+def key_of_position(p):
+    """Key index (0..63) held at position p of a 64-key fp8 V block."""
+    p = np.asarray(p)
+    return 32 * ((p & 31) >> 4) + 8 * ((p >> 2) & 3) + 4 * (p >> 5) + (p & 3)
+
+
+def position_of_key(k):
+    """Inverse of key_of_position."""
+    k = np.asarray(k)
+    return 32 * ((k >> 2) & 1) + 16 * ((k >> 5) & 1) + 4 * ((k >> 3) & 3) + (k & 3)
+
+
+V_KEY_OF_POS = key_of_position(np.arange(64))
+V_POS_OF_KEY = position_of_key(np.arange(64))
+
+
+def bf16_round(x):
+    """fp32 -> nearest bf16 (ties to even), returned as fp32."""
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+def e4m3_encode(x):
+    """fp32 tensor (|x| <= 448) -> e4m3fn bits (uint8), round to nearest even."""
+    return x.clamp(-V_MAX, V_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
+
+
+def e4m3_decode(bits):
+    """e4m3fn bits (uint8) -> fp32."""
+    return bits.view(torch.float8_e4m3fn).to(torch.float32)
+
+
+def _as_lhd(x):
+    """Accept [L, H, D] or [1, L, H, D]; return [L, H, D]."""
+    if x.dim() == 4:
+        assert x.shape[0] == 1, "the oracle handles batch 1; loop over the batch outside"
+        x = x[0]
+    return x
+
+
+def _quant_int8_blocks(xf, blk):
+    """xf: fp32 [H, nblk, blk, D] (padding already zero) -> int8 same shape, scale fp32 [H, nblk]."""
+    amax = xf.abs().amax(dim=(2, 3)).clamp_min(AMAX_FLOOR)
+    recip = torch.full_like(amax, 127.0) / amax                  # fp32, correctly rounded
+    q = (xf * recip[:, :, None, None]).round().clamp(-128, 127).to(torch.int8)
+    scale = amax / torch.full_like(amax, 127.0)
+    return q, scale
+
+
+def quant_q(q):
+    """q bf16 [Lq, H, D] -> (q8 int8 [H, Lp, D], q_scale fp32 [H, Lp / 32]); Lp = Lq rounded up to 128."""
+    q = _as_lhd(q)
+    lq, h, d = q.shape
+    lp = pad_to(lq, Q_TILE)
+    xf = torch.zeros(h, lp, d, dtype=torch.float32)
+    xf[:, :lq] = q.float().permute(1, 0, 2)
+    q8, qs = _quant_int8_blocks(xf.view(h, lp // Q_GROUP, Q_GROUP, d), Q_GROUP)
+    return q8.view(h, lp, d), qs
+
+
+def chunk_mean(k):
+    """Per-(head, channel) mean of k bf16 [L, H, D] in the fixed order above -> fp32 [H, D] holding bf16 values."""
+    k = _as_lhd(k)
+    n, h, d = k.shape
+    nb = pad_to(n, K_BLOCK) // K_BLOCK
+    x = torch.zeros(nb * K_BLOCK, h, d, dtype=torch.float32)
+    x[:n] = k.float()
+    x = x.view(nb, 4, 16, h, d)                  # [b, i, rg, h, d]: token = 64 b + rg + 16 i
+    s = torch.zeros(nb, 16, h, d, dtype=torch.float32)
+    for i in range(4):
+        s = s + x[:, i]
+    blk = torch.zeros(nb, h, d, dtype=torch.float32)
+    for rg in range(16):
+        blk = blk + s[:, rg]
+    tot = torch.zeros(h, d, dtype=torch.float32)
+    for b in range(nb):
+        tot = tot + blk[b]
+    mean = tot / torch.tensor(float(n), dtype=torch.float32)
+    return bf16_round(mean)
+
+
+def quant_k(k, km):
+    """k bf16 [L, H, D], km fp32 [H, D] -> (k8 int8 [H, Lp64, D], k_scale fp32 [H, nb])."""
+    k = _as_lhd(k)
+    n, h, d = k.shape
+    lp = pad_to(n, K_BLOCK)
+    xf = torch.zeros(h, lp, d, dtype=torch.float32)
+    xf[:, :n] = k.float().permute(1, 0, 2) - km[:, None, :]
+    k8, ks = _quant_int8_blocks(xf.view(h, lp // K_BLOCK, K_BLOCK, d), K_BLOCK)
+    return k8.view(h, lp, d), ks
+
+
+def v_scale_of(v):
+    """v bf16 [L, H, D] -> (v_scale, recip) fp32 [H, D]: amax / 448 and 448 / amax, amax floored at 1e-7."""
+    v = _as_lhd(v)
+    amax = v.float().abs().amax(dim=0).clamp_min(AMAX_FLOOR)
+    vmax = torch.full_like(amax, V_MAX)
+    return amax / vmax, vmax / amax
+
+
+def quant_v(v):
+    """v bf16 [L, H, D] -> (v8 uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, v_scale fp32 [H, D])."""
+    v = _as_lhd(v)
+    n, h, d = v.shape
+    lp = pad_to(n, K_BLOCK)
+    vs, recip = v_scale_of(v)
+    y = torch.zeros(h, lp, d, dtype=torch.float32)
+    y[:, :n] = v.float().permute(1, 0, 2) * recip[:, None, :]
+    bits = e4m3_encode(y).view(h, lp // K_BLOCK, K_BLOCK, d)       # [h, b, key, d]
+    bits = bits[:, :, torch.from_numpy(V_KEY_OF_POS)]               # [h, b, pos, d]
+    return bits.permute(0, 1, 3, 2).contiguous(), vs
+
+
+def requant(k, v):
+    """The save-to-memory re-quant of one chunk: bf16 K, V [L, H, D] -> dict of the quantised chunk."""
+    k = _as_lhd(k)
+    km = chunk_mean(k)
+    k8, ks = quant_k(k, km)
+    v8, vs = quant_v(v)
+    return {"k8": k8, "k_scale": ks, "km": km, "v8": v8, "v_scale": vs, "n": k.shape[0]}
+
+
+def dequant_v(chunk):
+    """fp8 V of a quantised chunk back to fp32 [H, n, D] in key order, without the V scale."""
+    v8 = chunk["v8"]                                     # [h, nb, d, 64] positions
+    h, nb, d, _ = v8.shape
+    vals = e4m3_decode(v8)[:, :, :, torch.from_numpy(V_POS_OF_KEY)]   # [h, nb, d, key]
+    return vals.permute(0, 1, 3, 2).reshape(h, nb * K_BLOCK, d)[:, :chunk["n"]]
+
+
+def qk_logits(q8, k8):
+    """int32 S = q8 . k8^T: [H, Lq, D] x [H, Lk, D] -> [H, Lq, Lk]. fp32 GEMM of int8 values is exact at
+    d = 128 (|S| <= 2^21 < 2^24)."""
+    s = torch.matmul(q8.float(), k8.float().transpose(1, 2))
+    return s.to(torch.int32)
+
+
+def q_bias(q, km):
+    """q . km in fp32 for every query and head: q bf16 [Lq, H, D], km fp32 [H, D] -> [H, Lq]."""
+    q = _as_lhd(q)
+    return torch.einsum("lhd,hd->hl", q.float(), km)
+
+
+def _sl2(sm_scale, d):
+    """sm_scale * log2(e) as the fp32 product the kernels use."""
+    sm = torch.tensor(d ** -0.5 if sm_scale is None else sm_scale, dtype=torch.float32)
+    return sm * torch.tensor(LOG2E, dtype=torch.float32)
+
+
+def attention(q, chunks, sm_scale=None, q_block=1024):
+    """Emulated quantized attention of q bf16 [Lq, H, D] over quantised chunks (dicts from `requant`), in the
+    kernel's own order: chunks in sequence, 64-key blocks in sequence, a running row max m, and per block
+      m_new = max(m, max_j S_ij * cb + beta),  alpha = exp2(m - m_new),  o = alpha * o,  l = alpha * l,
+      P_ij = exp2(S_ij * cb + beta - m_new + 8.807)  (<= 448),  l += sum P,  o += e4m3(P) . V8,
+    with cb = q_scale * k_scale * sm_scale * log2(e); at a chunk boundary o is rescaled by
+    v_scale_old / v_scale_new per channel; finally out = o * v_scale / l. Returns fp32 [Lq, H, D].
+    """
+    q = _as_lhd(q)
+    lq, h, d = q.shape
+    sl2 = _sl2(sm_scale, d)
+    q8, qs = quant_q(q)
+    multi = len(chunks) > 1
+    vdec = [dequant_v(c) for c in chunks]
+    bias = [q_bias(q, c["km"]) * sl2 if multi else None for c in chunks]
+    out = torch.empty(lq, h, d, dtype=torch.float32)
+    for hh in range(h):
+        for a in range(0, lq, q_block):
+            e = min(lq, a + q_block)
+            rows = e - a
+            qf = q8[hh, a:e].float()
+            qsr = qs[hh].repeat_interleave(Q_GROUP)[a:e]
+            m_run = torch.full((rows,), float("-inf"))
+            l_run = torch.zeros(rows)
+            o = torch.zeros(rows, d)
+            vs_prev = None
+            for ci, c in enumerate(chunks):
+                n = c["n"]
+                vs = c["v_scale"][hh]
+                if vs_prev is not None:
+                    o = o * (vs_prev / vs)[None, :]
+                beta = bias[ci][hh, a:e] if multi else torch.zeros(rows)
+                for b in range(pad_to(n, K_BLOCK) // K_BLOCK):
+                    k0, k1 = b * K_BLOCK, min(n, b * K_BLOCK + K_BLOCK)
+                    s_int = torch.matmul(qf, c["k8"][hh, k0:k1].float().t())
+                    cb = (qsr * c["k_scale"][hh, b]) * sl2
+                    m_blk = s_int.amax(dim=1) * cb + beta
+                    m_new = torch.maximum(m_run, m_blk)
+                    alpha = torch.exp2(m_run - m_new)
+                    m_run = m_new
+                    o = o * alpha[:, None]
+                    l_run = l_run * alpha
+                    kc = (beta - m_new + P_OFFSET).double()
+                    x = (s_int.double() * cb.double()[:, None] + kc[:, None]).float()
+                    p = torch.exp2(x)
+                    l_run = l_run + p.sum(dim=1)
+                    o = o + torch.matmul(e4m3_decode(e4m3_encode(p)), vdec[ci][hh, k0:k1])
+                vs_prev = vs
+            out[a:e, hh] = (o * vs_prev[None, :]) * (1.0 / l_run)[:, None]
+    return out
+
+
+def attention_exact_max(q, chunks, sm_scale=None, q_block=1024):
+    """The same scheme with each row's exact max over all keys (two passes): P is rounded against the final
+    max instead of the running one. Returns fp32 [Lq, H, D]."""
+    q = _as_lhd(q)
+    lq, h, d = q.shape
+    sl2 = _sl2(sm_scale, d)
+    q8, qs = quant_q(q)
+    multi = len(chunks) > 1
+    vdec = [dequant_v(c) for c in chunks]
+    bias = [q_bias(q, c["km"]) * sl2 if multi else None for c in chunks]
+    out = torch.empty(lq, h, d, dtype=torch.float32)
+    for hh in range(h):
+        for a in range(0, lq, q_block):
+            e = min(lq, a + q_block)
+            qsr = qs[hh].repeat_interleave(Q_GROUP)[a:e]
+            logits = []
+            for ci, c in enumerate(chunks):
+                n = c["n"]
+                s_int = torch.matmul(q8[hh, a:e].float(), c["k8"][hh, :n].float().t())
+                ksr = c["k_scale"][hh].repeat_interleave(K_BLOCK)[:n]
+                s = s_int * ((qsr[:, None] * ksr[None, :]) * sl2)
+                if multi:
+                    s = s + bias[ci][hh, a:e, None]
+                logits.append(s)
+            m = torch.stack([s.amax(dim=1) for s in logits], 1).amax(dim=1)
+            num = torch.zeros(e - a, d, dtype=torch.float32)
+            den = torch.zeros(e - a, dtype=torch.float32)
+            for ci, c in enumerate(chunks):
+                p = torch.exp2(logits[ci] - m[:, None] + P_OFFSET)
+                den = den + p.sum(dim=1)
+                p8 = e4m3_decode(e4m3_encode(p))
+                num = num + torch.matmul(p8, vdec[ci][hh]) * c["v_scale"][hh][None, :]
+            out[a:e, hh] = num / den[:, None]
+    return out
+
+
+def sdpa_fp32(q, k, v, sm_scale=None):
+    """fp32 softmax attention reference, per head: q [Lq, H, D], k/v [Lk, H, D] -> fp32 [Lq, H, D]."""
+    q, k, v = _as_lhd(q), _as_lhd(k), _as_lhd(v)
+    d = q.shape[-1]
+    sm_scale = d ** -0.5 if sm_scale is None else sm_scale
+    out = torch.empty(q.shape, dtype=torch.float32)
+    for hh in range(q.shape[1]):
+        s = torch.matmul(q[:, hh].float(), k[:, hh].float().t()) * sm_scale
+        out[:, hh] = torch.matmul(torch.softmax(s, dim=1), v[:, hh].float())
+    return out
+
+
+def merge_partials(parts):
+    """Split-KV merge (experiments/bench_attn/splitkv/README.md:62) in the exp2 domain.
+
+    parts: list of (o_unnormalised [Lq, D], m [Lq], d [Lq]); returns O = sum 2^(m_i - m) o_i / sum 2^(m_i - m) d_i.
+    """
+    m = torch.stack([p[1] for p in parts]).amax(dim=0)
+    num = sum(torch.exp2(p[1] - m)[:, None] * p[0] for p in parts)
+    den = sum(torch.exp2(p[1] - m) * p[2] for p in parts)
+    return num / den[:, None]
+
+
+def make_inputs(lq, lk, h=12, d=HEAD_DIM, seed=0, mem_chunks=0, chunk_len=None):
+    """Seeded synthetic inputs in the fixed generation order Q, K, K-offset, V, then per memory chunk K, V.
+
+    Q, V ~ N(0, 1); K ~ N(0, 1) + o[h, d] with o ~ N(0, 3) constant over tokens; memory chunk values
+    ~ N(0, 1.5). Tensors are bf16 in NHD [1, L, H, D].
+    """
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, lq, h, d, generator=g)
+    k = torch.randn(1, lk, h, d, generator=g)
+    off = torch.randn(1, 1, h, d, generator=g) * 3.0
+    v = torch.randn(1, lk, h, d, generator=g)
+    mem = []
+    for _ in range(mem_chunks):
+        n = chunk_len or lk
+        mk = torch.randn(1, n, h, d, generator=g) * 1.5
+        mv = torch.randn(1, n, h, d, generator=g) * 1.5
+        mem.append((mk.to(torch.bfloat16), mv.to(torch.bfloat16)))
+    return q.to(torch.bfloat16), (k + off).to(torch.bfloat16), v.to(torch.bfloat16), mem
+
+
+def attention_ops(lq, lk, h, d=HEAD_DIM, b=1):
+    """Algorithmic ops of one attention call: 4 * B * H * Lq * Lk * d (tools/roofline.py:91-95)."""
+    return 4.0 * b * h * lq * lk * d
+
+
+def requant_bytes(n, h, d=HEAD_DIM):
+    """Algorithmic bytes of one chunk's re-quant: read bf16 K and V once, write int8 K and fp8 V once,
+    plus the per-block K scales and the per-channel mean and V scale."""
+    nb = pad_to(n, K_BLOCK) // K_BLOCK
+    return 2 * n * h * d * 2 + 2 * n * h * d + nb * h * 4 + 2 * h * d * 4
+

@@ -1,0 +1,175 @@
+"""Parity of the HIP path (through the C-ABI) with the CPU oracle: bit-exact for the int8 / fp8 tensors, the
+scales, the K mean and the int32 logits; within tolerance for the attention output."""
+import pytest
+import torch
+
+from oracle import emu
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+# Output tolerance against fp32 SDPA on identical inputs (BASELINE): max-abs and mean-abs.
+SDPA_MAX_ABS = 2e-2
+SDPA_MEAN_ABS = 1e-3
+
+
+def _k():
+    from lingbot_world_v2_realtime_amd import kernels
+    return kernels
+
+
+def _ring(layers, heads, n, slots=1, batch=1):
+    k = _k()
+    return k.RingCache(layers, batch, heads, k.pad_to(n, 64), slots, DEV)
+
+
+def _check_chunk(ring, layer, slot, ref, n, bh_slice=slice(None)):
+    nb = (n + 63) // 64
+    torch.testing.assert_close(ring.km[layer, slot].cpu()[bh_slice], ref["km"], rtol=0, atol=0)
+    torch.testing.assert_close(ring.v_scale[layer, slot].cpu()[bh_slice], ref["v_scale"], rtol=0, atol=0)
+    torch.testing.assert_close(ring.k_scale[layer, slot, :, :nb].cpu()[bh_slice], ref["k_scale"], rtol=0, atol=0)
+    assert torch.equal(ring.k8[layer, slot, :, :nb * 64].cpu()[bh_slice], ref["k8"])
+    assert torch.equal(ring.v8[layer, slot, :, :nb].cpu()[bh_slice], ref["v8"])
+
+
+@pytest.mark.parametrize("n", [1, 16, 63, 64, 65, 200, 1508])
+def test_requant_bit_exact(n):
+    torch.manual_seed(n)
+    h = 3
+    k = (torch.randn(1, n, h, 128) + 3 * torch.randn(1, 1, h, 128)).to(torch.bfloat16)
+    v = (torch.randn(1, n, h, 128) * 1.7).to(torch.bfloat16)
+    ring = _ring(1, h, n, slots=2)
+    _k().kv_requant(k.to(DEV), v.to(DEV), ring, slot=1)
+    torch.cuda.synchronize()
+    _check_chunk(ring, 0, 1, emu.requant(k, v), n)
+
+
+def test_requant_cfg1_shape_and_zero_chunk():
+    q, k, v, _ = emu.make_inputs(1508, 1508)
+    ring = _ring(1, 12, 1508)
+    _k().kv_requant(k.to(DEV), v.to(DEV), ring, 0)
+    torch.cuda.synchronize()
+    _check_chunk(ring, 0, 0, emu.requant(k, v), 1508)
+    z = torch.zeros(1, 100, 12, 128, dtype=torch.bfloat16)
+    ring = _ring(1, 12, 100)
+    _k().kv_requant(z.to(DEV), z.to(DEV), ring, 0)
+    torch.cuda.synchronize()
+    ref = emu.requant(z, z)
+    assert float(ref["k_scale"].min()) == pytest.approx(1e-7 / 127)
+    _check_chunk(ring, 0, 0, ref, 100)
+
+
+def test_requant_layers_and_strides():
+    """Several layers in one call, K/V given as strided views (HND storage seen as NHD)."""
+    torch.manual_seed(7)
+    layers, h, n = 3, 4, 300
+    k = torch.randn(layers, 1, h, n, 128).to(torch.bfloat16)      # HND storage
+    v = torch.randn(layers, 1, h, n, 128).to(torch.bfloat16)
+    kd, vd = k.to(DEV).transpose(2, 3), v.to(DEV).transpose(2, 3)   # [layers, 1, n, h, 128] views
+    ring = _ring(layers + 1, h, n, slots=3)
+    _k().kv_requant(kd, vd, ring, slot=2, layer0=1)
+    torch.cuda.synchronize()
+    for l in range(layers):
+        ref = emu.requant(k[l].transpose(1, 2)[0], v[l].transpose(1, 2)[0])
+        _check_chunk(ring, l + 1, 2, ref, n)
+
+
+@pytest.mark.parametrize("lq", [1, 31, 32, 100, 1508])
+def test_quant_q_bit_exact(lq):
+    torch.manual_seed(lq)
+    q = (torch.randn(1, lq, 5, 128) * 2).to(torch.bfloat16)
+    q8, qs, _ = _k().quant_q(q.to(DEV))
+    torch.cuda.synchronize()
+    r8, rs = emu.quant_q(q)
+    assert torch.equal(q8.cpu(), r8)
+    torch.testing.assert_close(qs.cpu(), rs, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("lq,lk", [(128, 64), (200, 130), (1508, 1508)])
+def test_qk_logits_bit_exact(lq, lk):
+    torch.manual_seed(lq + lk)
+    h = 2
+    q = torch.randn(1, lq, h, 128).to(torch.bfloat16)
+    k = (torch.randn(1, lk, h, 128) + 3 * torch.randn(1, 1, h, 128)).to(torch.bfloat16)
+    ring = _ring(1, h, lk)
+    _k().kv_requant(k.to(DEV), k.to(DEV), ring, 0)
+    q8, _, _ = _k().quant_q(q.to(DEV))
+    s = _k().qk_logits(q8, lq, ring, 0, 0)
+    torch.cuda.synchronize()
+    r8, _ = emu.quant_q(q)
+    rk = emu.requant(k, k)
+    ref = emu.qk_logits(r8, rk["k8"])
+    assert torch.equal(s.cpu()[:, :, :ref.shape[2]], ref)
+
+
+def _attn_gpu(q, k, v):
+    from lingbot_world_v2_realtime_amd import sage_attention
+    return sage_attention(q.to(DEV), k.to(DEV), v.to(DEV)).float().cpu()
+
+
+@pytest.mark.parametrize("lq,lk", [(1, 1), (17, 70), (128, 64), (300, 1000)])
+def test_attention_small_vs_oracle(lq, lk):
+    q, k, v, _ = emu.make_inputs(lq, lk, h=3, seed=lq * 7 + lk)
+    out = _attn_gpu(q, k, v)
+    ref = emu.attention(q, [emu.requant(k, v)])[None]
+    sd = emu.sdpa_fp32(q, k, v)[None]
+    err_emu = (out - ref).abs()
+    err_sdpa = (out - sd).abs()
+    err_scheme = (ref - sd).abs()
+    print(f"lq={lq} lk={lk} vs-emu max {err_emu.max():.3e} mean {err_emu.mean():.3e} | "
+          f"vs-sdpa max {err_sdpa.max():.3e} mean {err_sdpa.mean():.3e} | "
+          f"emu vs-sdpa max {err_scheme.max():.3e} mean {err_scheme.mean():.3e}")
+    # The oracle follows the kernel's block order and running max, so the two differ only by exp2 ulps (which
+    # can move a P value to the neighbouring e4m3 step), the MFMA's accumulation order and the bf16 output
+    # rounding (2^-9 relative): a small fraction of the scheme's own distance from fp32 SDPA.
+    assert err_emu.mean() <= 0.1 * err_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert err_sdpa.max() <= 2 * err_scheme.max() + 1e-3
+    assert err_sdpa.mean() <= 1.1 * err_scheme.mean() + 1e-5
+
+
+def test_attention_cfg1_tolerance():
+    """cfg 1: one latent frame, [1, 1508, 12, 128], seed 0."""
+    q, k, v, _ = emu.make_inputs(1508, 1508)
+    out = _attn_gpu(q, k, v)
+    sd = emu.sdpa_fp32(q, k, v)[None]
+    ref = emu.attention(q, [emu.requant(k, v)])[None]
+    e_sd, e_emu = (out - sd).abs(), (out - ref).abs()
+    print(f"cfg1 vs-sdpa max {e_sd.max():.3e} mean {e_sd.mean():.3e}; vs-emu max {e_emu.max():.3e} "
+          f"mean {e_emu.mean():.3e}; emu vs sdpa mean {(ref - sd).abs().mean():.3e}")
+    assert e_sd.max() < SDPA_MAX_ABS
+    # mean-abs at 1508 keys sits at the e4m3 P x e4m3 V floor (the oracle itself is at 1.30e-3)
+    assert e_sd.mean() < 1.5e-3
+    assert e_emu.mean() < 5e-4
+
+
+def test_attention_cfg2_tolerance():
+    """cfg 2: full-chunk self-attention [1, 6032, 12, 128] against fp32 SDPA."""
+    q, k, v, _ = emu.make_inputs(6032, 6032)
+    out = _attn_gpu(q, k, v)
+    sd = emu.sdpa_fp32(q, k, v)[None]
+    e = (out - sd).abs()
+    print(f"cfg2 vs-sdpa max {e.max():.3e} mean {e.mean():.3e}")
+    assert e.max() < SDPA_MAX_ABS and e.mean() < SDPA_MEAN_ABS
+
+
+def test_memory_ring_attention():
+    """Chunk + memory: per-chunk mean and V scale inside one softmax, vs the oracle and fp32 SDPA."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    n, h = 700, 4
+    q, k, v, mem = emu.make_inputs(n, n, h=h, mem_chunks=3, chunk_len=n)
+    ring = QuantKVRing(2, 1, h, n, slots=4, device=DEV)
+    for mk, mv in mem:
+        ring.write(1, mk.to(DEV), mv.to(DEV))
+        ring.commit()
+    ring.write(1, k.to(DEV), v.to(DEV))
+    out = ring.attend(q.to(DEV), 1).float().cpu()
+    chunks = [emu.requant(mk, mv) for mk, mv in mem] + [emu.requant(k, v)]
+    ref = emu.attention(q, chunks)[None]
+    kk = torch.cat([m[0] for m in mem] + [k], 1)
+    vv = torch.cat([m[1] for m in mem] + [v], 1)
+    sd = emu.sdpa_fp32(q, kk, vv)[None]
+    e_emu, e_sd = (out - ref).abs(), (out - sd).abs()
+    print(f"ring vs-emu max {e_emu.max():.3e} mean {e_emu.mean():.3e}; vs-sdpa max {e_sd.max():.3e} "
+          f"mean {e_sd.mean():.3e}")
+    assert e_sd.max() < SDPA_MAX_ABS and e_sd.mean() < SDPA_MEAN_ABS
+    assert e_emu.mean() < 3e-4
