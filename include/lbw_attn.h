@@ -95,14 +95,26 @@ int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the
  * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA, fp32 accumulation, V scale
  * and 1 / row sum applied at the end. Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
- * 126-127; experiments/modules/sage_kvq.py:107-110). seg_slot / seg_len are host arrays.
+ * 126-127; experiments/modules/sage_kvq.py:107-110). seg_slot / seg_len are host arrays. `workspace` holds
+ * lbw_attn_workspace_bytes() bytes (16-byte aligned); two kernels run: the attention over a persistent grid
+ * and a merge of the query tiles whose keys were split between workgroups.
  */
 int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias,
                  int64_t batch, int64_t lq, int64_t heads,
                  const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* v_scale,
                  int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
                  uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
-                 float sm_scale, void* stream);
+                 float sm_scale, void* workspace, void* stream);
+
+/* Bytes of scratch lbw_attn_fwd needs on the current device (partial results of query tiles whose key range
+ * is split between workgroups); independent of the problem size. */
+int64_t lbw_attn_workspace_bytes(void);
+
+/* Persistent workgroups per XCD that lbw_attn_fwd launches on the current device (two per CU). Query tiles
+ * are dealt to XCDs in 8 contiguous ranges and, within one, whole tiles go round-robin to these workgroups
+ * while each gets one; the remaining tiles' key blocks are cut into equal contiguous pieces, one per
+ * workgroup. Exposed so a checker can reproduce the pieces (each piece rounds P against its own running max). */
+int lbw_attn_workgroups_per_xcd(void);
 
 /*
  * Debug: int32 logits S[bh][i][j] = sum_d q8[bh][i][d] * k8[slot][bh][j][d] for i < Lp and j < cap, through

@@ -16,7 +16,9 @@ SIGNATURES = {
                               _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p]),
     "lbw_quant_q": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "lbw_attn_fwd": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p,
-                            _p, _i64, _i64, _i64, _f32, _p]),
+                            _p, _i64, _i64, _i64, _f32, _p, _p]),
+    "lbw_attn_workspace_bytes": (_i64, []),
+    "lbw_attn_workgroups_per_xcd": (_i32, []),
     "lbw_qk_logits_i32": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p]),
 }
 

@@ -1,39 +1,60 @@
 // Quantized attention forward for gfx950: int8 QK^T on v_mfma_i32_32x32x32_i8, online softmax in the exp2
 // domain, e4m3 P times e4m3 V on v_mfma_f32_32x32x64_f8f6f4, fp32 accumulation.
 //
-// Work decomposition: one workgroup of 4 waves per (128-query tile, batch*head); wave w owns queries
-// 32w .. 32w+31 of the tile. Each wave computes S^T = K Q^T (keys on the MFMA M axis, queries on N), so a
-// lane holds one query and 16 keys of each 32x32 S tile: the row max and row sum are in-lane plus one
-// exchange with lane ^ 32, and the S tile's register layout is directly the B operand (P^T) of the PV
-// product O^T = V^T P^T once the fp8 V block stores its keys in the matching position order.
+// Tile: 4 waves x 32 queries = 128 queries of one batch*head. Each wave computes S^T = K Q^T (keys on the MFMA
+// M axis, queries on N), so a lane holds one query and 16 keys of each 32x32 S tile: the row max and row sum
+// are in-lane plus one exchange with lane ^ 32 (v_permlane32_swap), and the S tile's register layout is directly
+// the B operand (P^T) of the PV product O^T = V^T P^T because the fp8 V block stores its keys in that order.
+// K / V blocks of 64 keys (8 KB each) stream through LDS, double buffered: the next block's global loads are in
+// flight while the current one is computed. The int32 accumulator starts at the bits of 1.5 * 2^23, so its
+// result reads directly as the float 12582912 + S (|S| <= 2^21): the int -> float conversion is free.
 //
-// K / V tiles of 64 keys (8 KB each) stream through LDS, double buffered; the next tile's global loads are
-// in flight while the current one is computed. The int32 accumulator starts at the bits of 1.5 * 2^23, so
-// its result reads directly as the float 12582912 + S (|S| <= 2^21) and the int -> float conversion is free.
+// Scheduling: a persistent grid of `gx` workgroups per XCD (workgroup g runs on XCD g % 8). The query tiles
+// (head-major, so one head's tiles are contiguous) are split into 8 contiguous ranges, one per XCD, so each
+// XCD's L2 holds the K/V of ~1.5 heads. Within an XCD, whole tiles are dealt round-robin while every workgroup
+// gets one; the remaining tiles' (tile, key block) units are cut into equal contiguous pieces, one per
+// workgroup. A piece that is not a whole tile leaves an unnormalised partial (O, running max, row sum) in the
+// workspace, and attn_merge_kernel combines the pieces of each split tile.
 #include "lbw_common.h"
 
 namespace lbw {
 
-struct SegTable {
-  int n;
-  int slot[LBW_MAX_SEGMENTS];
-  int len[LBW_MAX_SEGMENTS];
-};
+constexpr int XCDS = 8;
+constexpr int TILE_BYTES = KB * D;   // 8 KB: one 64-key K tile or one 64-key fp8 V block
 
 struct AttnArgs {
   int64_t lq, lp, bh, heads, cap, nbc;
   int64_t o_sb, o_st, o_sh;
-  float sl2;   // sm_scale * log2(e)
-  SegTable seg;
+  float sl2;                       // sm_scale * log2(e)
+  int n_seg, nb, q_tiles, n_tiles, gx;
+  int seg_slot[LBW_MAX_SEGMENTS];
+  int seg_len[LBW_MAX_SEGMENTS];
+  int seg_blk0[LBW_MAX_SEGMENTS + 1];   // first tile-relative block of each chunk; [n_seg] = nb
 };
 
-constexpr int TILE_BYTES = KB * D;   // 8 KB: one 64-key K tile, or one 64-key fp8 V block
+// Range of tiles of XCD x and its data-parallel / split phases.
+struct XcdPlan {
+  int t_lo, t_hi, ts;   // tiles [t_lo, t_hi); tiles from ts on are split into pieces
+  int64_t units;        // (t_hi - ts) * nb
+};
+
+__device__ __forceinline__ XcdPlan xcd_plan(const AttnArgs& a, int x) {
+  XcdPlan p;
+  p.t_lo = (int)((int64_t)x * a.n_tiles / XCDS);
+  p.t_hi = (int)((int64_t)(x + 1) * a.n_tiles / XCDS);
+  const int rounds = (p.t_hi - p.t_lo) / a.gx;
+  p.ts = p.t_lo + rounds * a.gx;
+  p.units = (int64_t)(p.t_hi - p.ts) * a.nb;
+  return p;
+}
 
 // LDS byte offset of 16-byte chunk `ch` (0..7) of K row `row` (0..63): rows of 128 bytes, chunk index
 // xor-swizzled with the row so the 32 rows an MFMA A-operand read touches spread over the banks.
 __device__ __forceinline__ int k_lds_off(int row, int ch) { return row * 128 + ((ch ^ (row & 7)) << 4); }
 // LDS byte offset of 16-byte chunk `ch` (0..3) of V row (channel) `row` (0..127): rows of 64 bytes.
-__device__ __forceinline__ int v_lds_off(int row, int ch) { return TILE_BYTES + row * 64 + ((ch ^ ((row >> 1) & 3)) << 4); }
+__device__ __forceinline__ int v_lds_off(int row, int ch) {
+  return TILE_BYTES + row * 64 + ((ch ^ ((row >> 1) & 3)) << 4);
+}
 
 // S^T tile pair for 64 keys x 32 queries of this wave: acc[mt] covers keys 32 mt .. 32 mt + 31.
 __device__ __forceinline__ void qk_tile(const uint8_t* sk, const v4i* qf, int lq, int g, v16i* acc, int init) {
@@ -52,80 +73,114 @@ __device__ __forceinline__ void qk_tile(const uint8_t* sk, const v4i* qf, int lq
   }
 }
 
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const int8_t* __restrict__ q8,
-                                                       const float* __restrict__ q_scale,
-                                                       const float* __restrict__ bias,
-                                                       const int8_t* __restrict__ k8,
-                                                       const float* __restrict__ k_scale,
-                                                       const uint8_t* __restrict__ v8,
-                                                       const float* __restrict__ v_scale,
-                                                       uint16_t* __restrict__ out, AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * TILE_BYTES];
-  const int tile = blockIdx.x, bh = blockIdx.y;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, lq = lane & 31, g = lane >> 5;
-  const int64_t q0 = (int64_t)tile * QT + w * 32;
+// max / sum of a value over the two lane halves (lanes l and l ^ 32 hold the same query)
+__device__ __forceinline__ float halves_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
-  // Q^T B-operand fragments: lane (query lq, half g) holds channels 64 g .. 64 g + 63.
+__device__ __forceinline__ float max32(const float* f) {
+  float a[11];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) a[i] = fmaxf(fmaxf(f[3 * i], f[3 * i + 1]), f[3 * i + 2]);
+  a[10] = fmaxf(f[30], f[31]);
+  const float b0 = fmaxf(fmaxf(a[0], a[1]), a[2]), b1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
+  const float b2 = fmaxf(fmaxf(a[6], a[7]), a[8]), b3 = fmaxf(a[9], a[10]);
+  return fmaxf(fmaxf(b0, b1), fmaxf(b2, b3));
+}
+
+__device__ __forceinline__ float sum32(const float* p) {
+  float s[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s[i] = p[2 * i] + p[2 * i + 1];
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; ++i) s[i] = s[2 * i] + s[2 * i + 1];
+  return s[0];
+}
+
+struct Piece {      // online-softmax state of one wave after a range of key blocks
+  v16f o[4];        // O^T accumulator, units of the last chunk's V scale
+  float m, l;       // running max (log2 domain, bias included) and row sum (both lane halves combined)
+  int c_last;       // chunk of the last block processed
+};
+
+// Key blocks [j0, j1) of one tile for this wave's 32 queries.
+__device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __restrict__ q8,
+                                             const float* __restrict__ q_scale, const float* __restrict__ bias,
+                                             const int8_t* __restrict__ k8, const float* __restrict__ k_scale,
+                                             const uint8_t* __restrict__ v8, const float* __restrict__ v_scale,
+                                             uint8_t (*smem)[2 * TILE_BYTES], int bh, int64_t q0, int j0, int j1,
+                                             Piece& st) {
+  const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
   v4i qf[4];
   {
     const int8_t* qrow = q8 + ((int64_t)bh * a.lp + q0 + lq) * D + 64 * g;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *(const v4i*)(qrow + 16 * kk);
   }
-  const float qs = q_scale[(int64_t)bh * (a.lp / QG) + (q0 >> 5)];
-
-  v16f o[4];
+  const float qs_sl2 = q_scale[(int64_t)bh * (a.lp / QG) + (q0 >> 5)] * a.sl2;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) o[mt][i] = 0.f;
+    for (int i = 0; i < 16; ++i) st.o[mt][i] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
+  // chunk and chunk-relative block of j0
+  int c = 0;
+  while (j0 >= a.seg_blk0[c + 1]) ++c;
+  int blk = j0 - a.seg_blk0[c];
+  const bool multi = a.n_seg > 1;
+
   v4i pk0, pk1, pv0, pv1;
-  auto gload = [&](int c, int blk) {
-    const int64_t sbh = (int64_t)a.seg.slot[c] * a.bh + bh;
-    const int8_t* kp = k8 + (sbh * a.cap + (int64_t)blk * KB) * D;
-    const uint8_t* vp = v8 + (sbh * a.nbc + blk) * TILE_BYTES;
+  float ks_next = 0.f;
+  auto gload = [&](int cc, int bb) {
+    const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
+    const int8_t* kp = k8 + (sbh * a.cap + (int64_t)bb * KB) * D;
+    const uint8_t* vp = v8 + (sbh * a.nbc + bb) * TILE_BYTES;
     pk0 = *(const v4i*)(kp + t * 16);
     pk1 = *(const v4i*)(kp + 4096 + t * 16);
     pv0 = *(const v4i*)(vp + t * 16);
     pv1 = *(const v4i*)(vp + 4096 + t * 16);
+    ks_next = k_scale[sbh * a.nbc + bb];
   };
   auto lstore = [&](uint8_t* s) {
-    {
-      const int id0 = t, id1 = t + 256;
-      *(v4i*)(s + k_lds_off(id0 >> 3, id0 & 7)) = pk0;
-      *(v4i*)(s + k_lds_off(id1 >> 3, id1 & 7)) = pk1;
-      *(v4i*)(s + v_lds_off(id0 >> 2, id0 & 3)) = pv0;
-      *(v4i*)(s + v_lds_off(id1 >> 2, id1 & 3)) = pv1;
-    }
+    const int id0 = t, id1 = t + 256;
+    *(v4i*)(s + k_lds_off(id0 >> 3, id0 & 7)) = pk0;
+    *(v4i*)(s + k_lds_off(id1 >> 3, id1 & 7)) = pk1;
+    *(v4i*)(s + v_lds_off(id0 >> 2, id0 & 3)) = pv0;
+    *(v4i*)(s + v_lds_off(id1 >> 2, id1 & 3)) = pv1;
   };
 
-  int c = 0, blk = 0, buf = 0;
-  const bool multi = a.seg.n > 1;
-  float beta = multi ? bias[(int64_t)bh * a.lp + q0 + lq] * a.sl2 : 0.f;
-  gload(0, 0);
+  float beta = multi ? bias[((int64_t)c * a.bh + bh) * a.lp + q0 + lq] * a.sl2 : 0.f;
+  gload(c, blk);
+  float ks = ks_next;
   lstore(smem[0]);
   __syncthreads();
+  int buf = 0;
 
-  for (;;) {
+  for (int j = j0; j < j1; ++j) {
     int cn = c, bn = blk + 1;
-    if (bn * KB >= a.seg.len[c]) { cn = c + 1; bn = 0; }
-    const bool more = cn < a.seg.n;
+    if (j + 1 >= a.seg_blk0[c + 1]) { cn = c + 1; bn = 0; }
+    const bool more = j + 1 < j1;
     if (more) gload(cn, bn);
 
     const uint8_t* sk = smem[buf];
     v16i acc[2];
     qk_tile(sk, qf, lq, g, acc, S_MAGIC);
 
-    const int64_t sbh = (int64_t)a.seg.slot[c] * a.bh + bh;
-    const float cb = qs * k_scale[sbh * a.nbc + blk] * a.sl2;
+    const float cb = qs_sl2 * ks;
     float f[32];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) f[16 * mt + i] = __int_as_float(acc[mt][i]);
-    const int valid = a.seg.len[c] - blk * KB;   // keys of this block that exist (>= 1)
+    const int valid = a.seg_len[c] - blk * KB;   // keys of this block that exist (>= 1)
     if (valid < KB) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -135,28 +190,23 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const int8_t* __restrict_
           if (key >= valid) f[16 * mt + i] = -INFINITY;
         }
     }
-    float mx = f[0];
-#pragma unroll
-    for (int i = 1; i < 32; ++i) mx = fmaxf(mx, f[i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mx = halves_max(max32(f));
     const float m_blk = (mx - S_MAGIC_F) * cb + beta;
     const float m_new = fmaxf(m_run, m_blk);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
+    if (__any(m_new > m_run)) {   // wave-uniform: rescale only when some row's max moved
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+      for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[mt][i] *= alpha;
-    const float kc = (beta - m_new + P_OFFSET) - S_MAGIC_F * cb;
-    float p[32];
-    float ls = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(fmaf(f[i], cb, kc));
-      ls += p[i];
+        for (int i = 0; i < 16; ++i) st.o[mt][i] *= alpha;
+      m_run = m_new;
     }
-    l_run += ls;
+    const float kc = (beta - m_run + P_OFFSET) - S_MAGIC_F * cb;
+    float p[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(f[i], cb, kc));
+    l_run += sum32(p);
     // P^T B operand: byte 16 mt' + 4 i + j of this lane = p[16 mt' + 4 i + j] (keys 32 mt' + 8 i + 4 g + j).
     v8i pb;
 #pragma unroll
@@ -171,7 +221,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const int8_t* __restrict_
       const v4i lo = *(const v4i*)(sk + v_lds_off(row, 2 * g));
       const v4i hi = *(const v4i*)(sk + v_lds_off(row, 2 * g + 1));
       const v8i vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, o[mt], 0, 0, 0, 0, 0, 0);
+      st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[mt], 0, 0, 0, 0, 0, 0);
     }
 
     if (more) lstore(smem[buf ^ 1]);
@@ -179,41 +229,168 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const int8_t* __restrict_
     if (!more) break;
     if (cn != c) {
       // next chunk: its own V scale (rescale the accumulator per channel) and its own logit bias
-      const float* vs_old = v_scale + sbh * D;
-      const float* vs_new = v_scale + ((int64_t)a.seg.slot[cn] * a.bh + bh) * D;
+      const float* vs_old = v_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * D;
+      const float* vs_new = v_scale + ((int64_t)a.seg_slot[cn] * a.bh + bh) * D;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int ch = 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
-          o[mt][i] *= vs_old[ch] / vs_new[ch];
+          st.o[mt][i] *= vs_old[ch] / vs_new[ch];
         }
       beta = bias[((int64_t)cn * a.bh + bh) * a.lp + q0 + lq] * a.sl2;
     }
     c = cn;
     blk = bn;
+    ks = ks_next;
     buf ^= 1;
   }
+  st.m = m_run;
+  st.l = halves_sum(l_run);
+  st.c_last = c;
+}
 
-  // epilogue: O = o * v_scale / l, bf16, lane (query lq) writes channels 32 mt + 8 i + 4 g + (0..3)
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv_l = 1.f / l_tot;
+// Whole tile: O = o * v_scale / l as bf16; lane (query lq) writes channels 32 mt + 8 i + 4 g + (0..3).
+__device__ __forceinline__ void store_out(const AttnArgs& a, const Piece& st, const float* __restrict__ v_scale,
+                                          uint16_t* __restrict__ out, int bh, int64_t q0) {
+  const int lane = threadIdx.x & 63, lq = lane & 31, g = lane >> 5;
   const int64_t qrow = q0 + lq;
-  if (qrow < a.lq) {
-    const int64_t b = bh / a.heads, h = bh % a.heads;
-    uint16_t* op = out + b * a.o_sb + qrow * a.o_st + h * a.o_sh;
-    const float* vs = v_scale + ((int64_t)a.seg.slot[c] * a.bh + bh) * D;
+  if (qrow >= a.lq) return;
+  const float inv_l = 1.f / st.l;
+  const int64_t b = bh / a.heads, h = bh % a.heads;
+  uint16_t* op = out + b * a.o_sb + qrow * a.o_st + h * a.o_sh;
+  const float* vs = v_scale + ((int64_t)a.seg_slot[st.c_last] * a.bh + bh) * D;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int ch = 32 * mt + 8 * i + 4 * g;
-        uint32_t w0 = f32_to_bf16_bits(o[mt][4 * i] * vs[ch] * inv_l) |
-                      ((uint32_t)f32_to_bf16_bits(o[mt][4 * i + 1] * vs[ch + 1] * inv_l) << 16);
-        uint32_t w1 = f32_to_bf16_bits(o[mt][4 * i + 2] * vs[ch + 2] * inv_l) |
-                      ((uint32_t)f32_to_bf16_bits(o[mt][4 * i + 3] * vs[ch + 3] * inv_l) << 16);
-        *(uint2*)(op + ch) = make_uint2(w0, w1);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int ch = 32 * mt + 8 * i + 4 * g;
+      const uint32_t w0 = f32_to_bf16_bits(st.o[mt][4 * i] * vs[ch] * inv_l) |
+                          ((uint32_t)f32_to_bf16_bits(st.o[mt][4 * i + 1] * vs[ch + 1] * inv_l) << 16);
+      const uint32_t w1 = f32_to_bf16_bits(st.o[mt][4 * i + 2] * vs[ch + 2] * inv_l) |
+                          ((uint32_t)f32_to_bf16_bits(st.o[mt][4 * i + 3] * vs[ch + 3] * inv_l) << 16);
+      *(uint2*)(op + ch) = make_uint2(w0, w1);
+    }
+}
+
+// Part of a tile: o * v_scale (unnormalised) and (m, l) per row into workspace slot (g, slot).
+__device__ __forceinline__ void store_part(const AttnArgs& a, const Piece& st, const float* __restrict__ v_scale,
+                                           float* __restrict__ o_part, float* __restrict__ ml_part, int bh,
+                                           int64_t slot_idx, int w) {
+  const int lane = threadIdx.x & 63, lq = lane & 31, g = lane >> 5;
+  const int row = w * 32 + lq;
+  float* op = o_part + (slot_idx * QT + row) * D;
+  const float* vs = v_scale + ((int64_t)a.seg_slot[st.c_last] * a.bh + bh) * D;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ch = 32 * mt + 8 * i + 4 * g;
+      float4 v;
+      v.x = st.o[mt][4 * i] * vs[ch];
+      v.y = st.o[mt][4 * i + 1] * vs[ch + 1];
+      v.z = st.o[mt][4 * i + 2] * vs[ch + 2];
+      v.w = st.o[mt][4 * i + 3] * vs[ch + 3];
+      *(float4*)(op + ch) = v;
+    }
+  if (g == 0) *(float2*)(ml_part + (slot_idx * QT + row) * 2) = make_float2(st.m, st.l);
+}
+
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restrict__ q8,
+                                                          const float* __restrict__ q_scale,
+                                                          const float* __restrict__ bias,
+                                                          const int8_t* __restrict__ k8,
+                                                          const float* __restrict__ k_scale,
+                                                          const uint8_t* __restrict__ v8,
+                                                          const float* __restrict__ v_scale,
+                                                          uint16_t* __restrict__ out, float* __restrict__ o_part,
+                                                          float* __restrict__ ml_part, AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * TILE_BYTES];
+  const int gid = blockIdx.x, x = gid % XCDS, i = gid / XCDS;
+  const int w = threadIdx.x >> 6;
+  const XcdPlan p = xcd_plan(a, x);
+  Piece st;
+  // whole tiles, dealt round-robin among this XCD's workgroups
+  for (int tile = p.t_lo + i; tile < p.ts; tile += a.gx) {
+    const int bh = tile / a.q_tiles;
+    const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
+    attend_range(a, q8, q_scale, bias, k8, k_scale, v8, v_scale, smem, bh, q0, 0, a.nb, st);
+    store_out(a, st, v_scale, out, bh, q0);
+  }
+  // this workgroup's piece of the split tiles
+  if (p.units == 0) return;
+  const int64_t u0 = (int64_t)i * p.units / a.gx, u1 = (int64_t)(i + 1) * p.units / a.gx;
+  const int first_tile = p.ts + (int)(u0 / a.nb);
+  for (int64_t u = u0; u < u1;) {
+    const int tile = p.ts + (int)(u / a.nb);
+    const int j0 = (int)(u % a.nb);
+    const int j1 = (int)((u1 - u + j0 < a.nb) ? (u1 - u + j0) : a.nb);
+    const int bh = tile / a.q_tiles;
+    const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
+    attend_range(a, q8, q_scale, bias, k8, k_scale, v8, v_scale, smem, bh, q0, j0, j1, st);
+    if (j0 == 0 && j1 == a.nb) {
+      store_out(a, st, v_scale, out, bh, q0);
+    } else {
+      store_part(a, st, v_scale, o_part, ml_part, bh, (int64_t)gid * 2 + (tile == first_tile ? 0 : 1), w);
+    }
+    u += j1 - j0;
+  }
+}
+
+// Combine the pieces of each split tile: O = sum 2^(m_i - M) o_i / sum 2^(m_i - M) l_i
+// (experiments/bench_attn/splitkv/README.md:62). One workgroup per tile; thread = (row, 64-channel half).
+__global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ o_part,
+                                                         const float* __restrict__ ml_part,
+                                                         uint16_t* __restrict__ out, AttnArgs a) {
+  const int tile = blockIdx.x;
+  int x = 0;
+  while (x + 1 < XCDS && tile >= (int)((int64_t)(x + 1) * a.n_tiles / XCDS)) ++x;
+  const XcdPlan p = xcd_plan(a, x);
+  if (tile < p.ts) return;
+  const int64_t ua = (int64_t)(tile - p.ts) * a.nb, ub = ua + a.nb;
+  // workgroups of this XCD whose unit range meets [ua, ub): owner(u) = floor(((u + 1) gx - 1) / units)
+  const int i_a = (int)(((ua + 1) * a.gx - 1) / p.units);
+  const int i_b = (int)((ub * a.gx - 1) / p.units);
+  const int64_t i_a_u0 = (int64_t)i_a * p.units / a.gx, i_a_u1 = (int64_t)(i_a + 1) * p.units / a.gx;
+  if (i_a == i_b && i_a_u0 <= ua && i_a_u1 >= ub) return;   // written whole by one workgroup
+  const int t = threadIdx.x, row = t >> 1, half = t & 1;
+  const int64_t q = (int64_t)(tile % a.q_tiles) * QT + row;
+  if (q >= a.lq) return;
+  float mmax = -INFINITY;
+  for (int ii = i_a; ii <= i_b; ++ii) {
+    const int64_t w0 = (int64_t)ii * p.units / a.gx, w1 = (int64_t)(ii + 1) * p.units / a.gx;
+    if (w0 == w1 || w1 <= ua || w0 >= ub) continue;   // no units of this tile
+    const int ft = p.ts + (int)(w0 / a.nb);
+    const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (tile == ft ? 0 : 1);
+    mmax = fmaxf(mmax, ml_part[(slot * QT + row) * 2]);
+  }
+  float acc[64], den = 0.f;
+#pragma unroll
+  for (int c = 0; c < 64; ++c) acc[c] = 0.f;
+  for (int ii = i_a; ii <= i_b; ++ii) {
+    const int64_t w0 = (int64_t)ii * p.units / a.gx, w1 = (int64_t)(ii + 1) * p.units / a.gx;
+    if (w0 == w1 || w1 <= ua || w0 >= ub) continue;
+    const int ft = p.ts + (int)(w0 / a.nb);
+    const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (tile == ft ? 0 : 1);
+    const float2 ml = *(const float2*)(ml_part + (slot * QT + row) * 2);
+    const float wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
+    den += wgt * ml.y;
+    const float* op = o_part + (slot * QT + row) * D + half * 64;
+#pragma unroll
+    for (int c = 0; c < 64; c += 4) {
+      const float4 v = *(const float4*)(op + c);
+      acc[c] += wgt * v.x; acc[c + 1] += wgt * v.y; acc[c + 2] += wgt * v.z; acc[c + 3] += wgt * v.w;
+    }
+  }
+  const float inv = 1.f / den;
+  const int bh = tile / a.q_tiles;
+  const int64_t b = bh / a.heads, h = bh % a.heads;
+  uint16_t* dst = out + b * a.o_sb + q * a.o_st + h * a.o_sh + half * 64;
+#pragma unroll
+  for (int c = 0; c < 64; c += 4) {
+    const uint32_t w0 = f32_to_bf16_bits(acc[c] * inv) | ((uint32_t)f32_to_bf16_bits(acc[c + 1] * inv) << 16);
+    const uint32_t w1 = f32_to_bf16_bits(acc[c + 2] * inv) | ((uint32_t)f32_to_bf16_bits(acc[c + 3] * inv) << 16);
+    *(uint2*)(dst + c) = make_uint2(w0, w1);
   }
 }
 
@@ -244,23 +421,45 @@ __global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict
     for (int i = 0; i < 16; ++i) op[32 * mt + 8 * (i >> 2) + 4 * g + (i & 3)] = acc[mt][i];
 }
 
+// Persistent workgroups per XCD: two per CU (the kernel fits two 4-wave workgroups per CU).
+static int attn_wgs_per_xcd() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = (cus * 2 + XCDS - 1) / XCDS;
+  }
+  return cached[dev];
+}
+
 }  // namespace lbw
 
 using namespace lbw;
+
+extern "C" int lbw_attn_workgroups_per_xcd(void) { return attn_wgs_per_xcd(); }
+
+extern "C" int64_t lbw_attn_workspace_bytes(void) {
+  const int64_t gx = attn_wgs_per_xcd();
+  return (int64_t)XCDS * gx * 2 * QT * (D + 2) * (int64_t)sizeof(float);
+}
 
 extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
                             int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
                             const uint8_t* v8, const float* v_scale, int64_t slots, int64_t cap, int n_seg,
                             const int32_t* seg_slot, const int32_t* seg_len, uint16_t* out,
                             int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head, float sm_scale,
-                            void* stream) {
-  if (!q8 || !q_scale || !k8 || !k_scale || !v8 || !v_scale || !out || !seg_slot || !seg_len) return LBW_E_NULL;
+                            void* workspace, void* stream) {
+  if (!q8 || !q_scale || !k8 || !k_scale || !v8 || !v_scale || !out || !seg_slot || !seg_len || !workspace)
+    return LBW_E_NULL;
   if (batch <= 0 || heads <= 0 || lq <= 0 || slots <= 0 || cap <= 0 || cap % KB) return LBW_E_SHAPE;
-  if (batch * heads > 65535 || !(sm_scale > 0.f)) return LBW_E_SHAPE;
+  if (batch * heads > 65535 || !(sm_scale > 0.f) || lq > ((int64_t)1 << 30)) return LBW_E_SHAPE;
   if (n_seg < 1 || n_seg > LBW_MAX_SEGMENTS) return LBW_E_SEGMENTS;
   if (n_seg > 1 && !bias) return LBW_E_NULL;
   if (o_s_batch % 4 || o_s_tok % 4 || o_s_head % 4) return LBW_E_ALIGN;
-  if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v8) & 15 || ((uintptr_t)out & 7)) return LBW_E_ALIGN;
+  if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)workspace) & 15 || ((uintptr_t)out & 7))
+    return LBW_E_ALIGN;
   AttnArgs a;
   a.lq = lq;
   a.lp = (lq + QT - 1) / QT * QT;
@@ -270,15 +469,29 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   a.nbc = cap / KB;
   a.o_sb = o_s_batch; a.o_st = o_s_tok; a.o_sh = o_s_head;
   a.sl2 = sm_scale * 1.4426950408889634f;
-  a.seg.n = n_seg;
-  for (int c = 0; c < LBW_MAX_SEGMENTS; ++c) { a.seg.slot[c] = 0; a.seg.len[c] = 0; }
+  a.n_seg = n_seg;
+  int nb = 0;
+  for (int c = 0; c <= LBW_MAX_SEGMENTS; ++c) a.seg_blk0[c] = 0;
+  for (int c = 0; c < LBW_MAX_SEGMENTS; ++c) { a.seg_slot[c] = 0; a.seg_len[c] = 0; }
   for (int c = 0; c < n_seg; ++c) {
     if (seg_slot[c] < 0 || seg_slot[c] >= slots || seg_len[c] < 1 || seg_len[c] > cap) return LBW_E_SEGMENTS;
-    a.seg.slot[c] = seg_slot[c];
-    a.seg.len[c] = seg_len[c];
+    a.seg_slot[c] = seg_slot[c];
+    a.seg_len[c] = seg_len[c];
+    a.seg_blk0[c] = nb;
+    nb += (seg_len[c] + KB - 1) / KB;
   }
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(a.lp / QT), (unsigned)a.bh), dim3(256), 0,
-                     (hipStream_t)stream, q8, q_scale, bias, k8, k_scale, v8, v_scale, out, a);
+  for (int c = n_seg; c <= LBW_MAX_SEGMENTS; ++c) a.seg_blk0[c] = nb;
+  a.nb = nb;
+  a.q_tiles = (int)(a.lp / QT);
+  if ((int64_t)a.q_tiles * a.bh > 0x7fffffff / 2) return LBW_E_SHAPE;
+  a.n_tiles = (int)(a.q_tiles * a.bh);
+  a.gx = attn_wgs_per_xcd();
+  float* o_part = (float*)workspace;
+  float* ml_part = o_part + (int64_t)XCDS * a.gx * 2 * QT * D;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(XCDS * a.gx)), dim3(256), 0, st, q8, q_scale, bias, k8,
+                     k_scale, v8, v_scale, out, o_part, ml_part, a);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)a.n_tiles), dim3(256), 0, st, o_part, ml_part, out, a);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }

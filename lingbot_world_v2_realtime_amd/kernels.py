@@ -117,8 +117,21 @@ def quant_q(q, layout="NHD", ring=None, layer=0, seg_slots=()):
     return q8, qs, bias
 
 
+_ATTN_WS = {}
+
+
+def attn_workspace(device):
+    """The attention's scratch for `device` (partials of split query tiles), allocated once per device."""
+    dev = torch.device(device)
+    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    if key not in _ATTN_WS:
+        nbytes = _lib.load().lbw_attn_workspace_bytes()
+        _ATTN_WS[key] = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    return _ATTN_WS[key]
+
+
 def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_lens, out, layout="NHD",
-             sm_scale=None):
+             sm_scale=None, workspace=None):
     """Quantized attention of quantised Q over the chunks `seg_slots` (with `seg_lens` valid tokens) of one
     layer of `ring`, written into bf16 `out` ([B, Lq, H, 128] NHD or [B, H, Lq, 128] HND)."""
     lib = _lib.load()
@@ -130,9 +143,11 @@ def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_le
     k8, ksc, _, v8, vsc = ring.layer_view(layer)
     slot_arr = (ctypes_i32 * n_seg)(*seg_slots)
     len_arr = (ctypes_i32 * n_seg)(*seg_lens)
+    if workspace is None:
+        workspace = attn_workspace(q8.device)
     st = lib.lbw_attn_fwd(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
                           _ptr(v8), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr, _ptr(out),
-                          o_b, o_t, o_h, sm_scale, _stream(q8))
+                          o_b, o_t, o_h, sm_scale, _ptr(workspace), _stream(q8))
     _lib.check(st, "lbw_attn_fwd")
     return out
 

@@ -200,13 +200,79 @@ def _sl2(sm_scale, d):
     return sm * torch.tensor(LOG2E, dtype=torch.float32)
 
 
-def attention(q, chunks, sm_scale=None, q_block=1024):
+XCDS = 8
+
+
+def attn_schedule(n_tiles, nb, gx):
+    """Key-block pieces of every 128-query tile under the kernel's schedule: tiles (head-major) split into 8
+    contiguous per-XCD ranges; within a range whole tiles go round-robin to its `gx` workgroups while each
+    gets one, and the rest's (tile, block) units are cut into `gx` equal contiguous pieces.
+    Returns {tile: [(j0, j1), ...]} with pieces in increasing j0 (the merge order)."""
+    pieces = {t: [] for t in range(n_tiles)}
+    for x in range(XCDS):
+        t_lo, t_hi = x * n_tiles // XCDS, (x + 1) * n_tiles // XCDS
+        ts = t_lo + (t_hi - t_lo) // gx * gx
+        units = (t_hi - ts) * nb
+        for t in range(t_lo, ts):
+            pieces[t].append((0, nb))
+        for i in range(gx):
+            u, u1 = i * units // gx, (i + 1) * units // gx
+            while u < u1:
+                t, j0 = ts + u // nb, u % nb
+                j1 = min(nb, j0 + (u1 - u))
+                pieces[t].append((j0, j1))
+                u += j1 - j0
+    return pieces
+
+
+def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2):
+    """Online softmax over tile-relative key blocks [j0, j1) (numbered across the chunks in order) for the
+    query rows `qf` (q8 as fp32) -> (o in units of the last chunk's V scale, m, l, last chunk index)."""
+    rows, d = qf.shape[0], qf.shape[1]
+    m_run = torch.full((rows,), float("-inf"))
+    l_run = torch.zeros(rows)
+    o = torch.zeros(rows, d)
+    vs_prev, c_last, j = None, None, 0
+    for ci, c in enumerate(chunks):
+        n = c["n"]
+        nbc = pad_to(n, K_BLOCK) // K_BLOCK
+        if j + nbc <= j0 or j >= j1:
+            j += nbc
+            continue
+        vs = c["v_scale"][hh]
+        if vs_prev is not None:
+            o = o * (vs_prev / vs)[None, :]
+        beta = beta_of(ci)
+        for b in range(max(0, j0 - j), min(nbc, j1 - j)):
+            k0, k1 = b * K_BLOCK, min(n, b * K_BLOCK + K_BLOCK)
+            s_int = torch.matmul(qf, c["k8"][hh, k0:k1].float().t())
+            cb = (qsr * sl2) * c["k_scale"][hh, b]
+            m_blk = s_int.amax(dim=1) * cb + beta
+            m_new = torch.maximum(m_run, m_blk)
+            alpha = torch.exp2(m_run - m_new)
+            m_run = m_new
+            o = o * alpha[:, None]
+            l_run = l_run * alpha
+            kc = (beta - m_new + P_OFFSET).double()
+            x = (s_int.double() * cb.double()[:, None] + kc[:, None]).float()
+            p = torch.exp2(x)
+            l_run = l_run + p.sum(dim=1)
+            o = o + torch.matmul(e4m3_decode(e4m3_encode(p)), vdec[ci][hh, k0:k1])
+        vs_prev, c_last = vs, ci
+        j += nbc
+    return o, m_run, l_run, c_last
+
+
+def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None):
     """Emulated quantized attention of q bf16 [Lq, H, D] over quantised chunks (dicts from `requant`), in the
     kernel's own order: chunks in sequence, 64-key blocks in sequence, a running row max m, and per block
       m_new = max(m, max_j S_ij * cb + beta),  alpha = exp2(m - m_new),  o = alpha * o,  l = alpha * l,
       P_ij = exp2(S_ij * cb + beta - m_new + 8.807)  (<= 448),  l += sum P,  o += e4m3(P) . V8,
     with cb = q_scale * k_scale * sm_scale * log2(e); at a chunk boundary o is rescaled by
-    v_scale_old / v_scale_new per channel; finally out = o * v_scale / l. Returns fp32 [Lq, H, D].
+    v_scale_old / v_scale_new per channel; finally out = o * v_scale / l.
+    With `schedule_gx` (the kernel's workgroups per XCD), tiles the kernel splits between workgroups are
+    computed piece by piece from a fresh state and merged as O = sum 2^(m_i - M) o_i / sum 2^(m_i - M) l_i.
+    Returns fp32 [Lq, H, D].
     """
     q = _as_lhd(q)
     lq, h, d = q.shape
@@ -215,40 +281,50 @@ def attention(q, chunks, sm_scale=None, q_block=1024):
     multi = len(chunks) > 1
     vdec = [dequant_v(c) for c in chunks]
     bias = [q_bias(q, c["km"]) * sl2 if multi else None for c in chunks]
+    nb = sum(pad_to(c["n"], K_BLOCK) // K_BLOCK for c in chunks)
+    q_tiles = pad_to(lq, Q_TILE) // Q_TILE
+    sched = attn_schedule(q_tiles * h, nb, schedule_gx) if schedule_gx else None
     out = torch.empty(lq, h, d, dtype=torch.float32)
+    qsr_all = qs.repeat_interleave(Q_GROUP, dim=1)
     for hh in range(h):
-        for a in range(0, lq, q_block):
-            e = min(lq, a + q_block)
-            rows = e - a
+        # row ranges that run as one piece over all blocks, and the split tiles
+        split = set()
+        if sched is not None:
+            split = {t for t in range(q_tiles) if sched[hh * q_tiles + t] != [(0, nb)]}
+        ranges, a = [], 0
+        while a < lq:
+            t = a // Q_TILE
+            if t in split:
+                ranges.append((a, min(lq, a + Q_TILE), t))
+                a += Q_TILE
+            else:
+                e = min(lq, a + max(Q_TILE, q_block // Q_TILE * Q_TILE))
+                for tt in range(t, (e + Q_TILE - 1) // Q_TILE):
+                    if tt in split:
+                        e = tt * Q_TILE
+                        break
+                ranges.append((a, e, None))
+                a = e
+        for a, e, t in ranges:
             qf = q8[hh, a:e].float()
-            qsr = qs[hh].repeat_interleave(Q_GROUP)[a:e]
-            m_run = torch.full((rows,), float("-inf"))
-            l_run = torch.zeros(rows)
-            o = torch.zeros(rows, d)
-            vs_prev = None
-            for ci, c in enumerate(chunks):
-                n = c["n"]
-                vs = c["v_scale"][hh]
-                if vs_prev is not None:
-                    o = o * (vs_prev / vs)[None, :]
-                beta = bias[ci][hh, a:e] if multi else torch.zeros(rows)
-                for b in range(pad_to(n, K_BLOCK) // K_BLOCK):
-                    k0, k1 = b * K_BLOCK, min(n, b * K_BLOCK + K_BLOCK)
-                    s_int = torch.matmul(qf, c["k8"][hh, k0:k1].float().t())
-                    cb = (qsr * c["k_scale"][hh, b]) * sl2
-                    m_blk = s_int.amax(dim=1) * cb + beta
-                    m_new = torch.maximum(m_run, m_blk)
-                    alpha = torch.exp2(m_run - m_new)
-                    m_run = m_new
-                    o = o * alpha[:, None]
-                    l_run = l_run * alpha
-                    kc = (beta - m_new + P_OFFSET).double()
-                    x = (s_int.double() * cb.double()[:, None] + kc[:, None]).float()
-                    p = torch.exp2(x)
-                    l_run = l_run + p.sum(dim=1)
-                    o = o + torch.matmul(e4m3_decode(e4m3_encode(p)), vdec[ci][hh, k0:k1])
-                vs_prev = vs
-            out[a:e, hh] = (o * vs_prev[None, :]) * (1.0 / l_run)[:, None]
+            qsr = qsr_all[hh, a:e]
+            beta_of = (lambda ci: bias[ci][hh, a:e]) if multi else (lambda ci: torch.zeros(e - a))
+            if t is None:
+                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, 0, nb, sl2)
+                out[a:e, hh] = (o * chunks[cl]["v_scale"][hh][None, :]) * (1.0 / l)[:, None]
+                continue
+            parts = []
+            for j0, j1 in sched[hh * q_tiles + t]:
+                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2)
+                parts.append((o * chunks[cl]["v_scale"][hh][None, :], m, l))
+            mmax = torch.stack([pm for _, pm, _ in parts]).amax(dim=0)
+            num = torch.zeros(e - a, d)
+            den = torch.zeros(e - a)
+            for po, pm, pl in parts:
+                wgt = torch.exp2(pm - mmax)
+                den = den + wgt * pl
+                num = num + wgt[:, None] * po
+            out[a:e, hh] = num * (1.0 / den)[:, None]
     return out
 
 

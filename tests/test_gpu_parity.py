@@ -102,6 +102,11 @@ def test_qk_logits_bit_exact(lq, lk):
     assert torch.equal(s.cpu()[:, :, :ref.shape[2]], ref)
 
 
+def _gx():
+    from lingbot_world_v2_realtime_amd import _lib
+    return _lib.load().lbw_attn_workgroups_per_xcd()
+
+
 def _attn_gpu(q, k, v):
     from lingbot_world_v2_realtime_amd import sage_attention
     return sage_attention(q.to(DEV), k.to(DEV), v.to(DEV)).float().cpu()
@@ -111,7 +116,7 @@ def _attn_gpu(q, k, v):
 def test_attention_small_vs_oracle(lq, lk):
     q, k, v, _ = emu.make_inputs(lq, lk, h=3, seed=lq * 7 + lk)
     out = _attn_gpu(q, k, v)
-    ref = emu.attention(q, [emu.requant(k, v)])[None]
+    ref = emu.attention(q, [emu.requant(k, v)], schedule_gx=_gx())[None]
     sd = emu.sdpa_fp32(q, k, v)[None]
     err_emu = (out - ref).abs()
     err_sdpa = (out - sd).abs()
@@ -132,7 +137,7 @@ def test_attention_cfg1_tolerance():
     q, k, v, _ = emu.make_inputs(1508, 1508)
     out = _attn_gpu(q, k, v)
     sd = emu.sdpa_fp32(q, k, v)[None]
-    ref = emu.attention(q, [emu.requant(k, v)])[None]
+    ref = emu.attention(q, [emu.requant(k, v)], schedule_gx=_gx())[None]
     e_sd, e_emu = (out - sd).abs(), (out - ref).abs()
     print(f"cfg1 vs-sdpa max {e_sd.max():.3e} mean {e_sd.mean():.3e}; vs-emu max {e_emu.max():.3e} "
           f"mean {e_emu.mean():.3e}; emu vs sdpa mean {(ref - sd).abs().mean():.3e}")
@@ -164,12 +169,46 @@ def test_memory_ring_attention():
     ring.write(1, k.to(DEV), v.to(DEV))
     out = ring.attend(q.to(DEV), 1).float().cpu()
     chunks = [emu.requant(mk, mv) for mk, mv in mem] + [emu.requant(k, v)]
-    ref = emu.attention(q, chunks)[None]
+    ref = emu.attention(q, chunks, schedule_gx=_gx())[None]
     kk = torch.cat([m[0] for m in mem] + [k], 1)
     vv = torch.cat([m[1] for m in mem] + [v], 1)
     sd = emu.sdpa_fp32(q, kk, vv)[None]
-    e_emu, e_sd = (out - ref).abs(), (out - sd).abs()
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
     print(f"ring vs-emu max {e_emu.max():.3e} mean {e_emu.mean():.3e}; vs-sdpa max {e_sd.max():.3e} "
-          f"mean {e_sd.mean():.3e}")
-    assert e_sd.max() < SDPA_MAX_ABS and e_sd.mean() < SDPA_MEAN_ABS
-    assert e_emu.mean() < 3e-4
+          f"mean {e_sd.mean():.3e}; emu vs-sdpa max {e_scheme.max():.3e} mean {e_scheme.mean():.3e}")
+    # 700-key chunks with N(0, 1.5) memory values: the scheme's own error is above the full-shape gate, so
+    # the GPU is held to the oracle here and to fp32 SDPA at the real shape (test_attention_cfg3_tolerance).
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean()
+    assert e_sd.max() <= 2 * e_scheme.max()
+
+
+def _sdpa_gpu_fp32(q, k, v):
+    """fp32 softmax attention on the GPU, per head: [1, L, H, D] bf16 -> fp32 [1, Lq, H, D]."""
+    qd, kd, vd = (x.to(DEV).float() for x in (q, k, v))
+    out = torch.empty(qd.shape, dtype=torch.float32, device=DEV)
+    for hh in range(qd.shape[2]):
+        s = torch.matmul(qd[0, :, hh], kd[0, :, hh].t()) * (qd.shape[-1] ** -0.5)
+        out[0, :, hh] = torch.matmul(torch.softmax(s, dim=1), vd[0, :, hh])
+    return out
+
+
+def test_attention_cfg3_tolerance():
+    """cfg 3: Q [1, 6032, 12, 128] against 24128 keys = current chunk + 3 cached chunks (memory ~N(0, 1.5)),
+    each chunk quantised with its own mean and V scales, vs fp32 SDPA over the same bf16 keys and values."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    n, h = 6032, 12
+    q, k, v, mem = emu.make_inputs(n, n, h=h, mem_chunks=3, chunk_len=n)
+    ring = QuantKVRing(1, 1, h, n, slots=4, device=DEV)
+    for mk, mv in mem:
+        ring.write(0, mk.to(DEV), mv.to(DEV))
+        ring.commit()
+    ring.write(0, k.to(DEV), v.to(DEV))
+    out = ring.attend(q.to(DEV), 0).float()
+    kk = torch.cat([m[0] for m in mem] + [k], 1)
+    vv = torch.cat([m[1] for m in mem] + [v], 1)
+    sd = _sdpa_gpu_fp32(q, kk, vv)
+    e = (out - sd).abs()
+    print(f"cfg3 vs-sdpa max {e.max():.3e} mean {e.mean():.3e} (|out| mean {sd.abs().mean():.3e})")
+    assert e.mean() < SDPA_MEAN_ABS
+    assert e.max() < SDPA_MAX_ABS
