@@ -48,24 +48,27 @@ __device__ __forceinline__ XcdPlan xcd_plan(const AttnArgs& a, int x) {
   return p;
 }
 
-// LDS byte offset of 16-byte chunk `ch` (0..7) of K row `row` (0..63): rows of 128 bytes, chunk index
-// xor-swizzled with the row so the 32 rows an MFMA A-operand read touches spread over the banks.
-__device__ __forceinline__ int k_lds_off(int row, int ch) { return row * 128 + ((ch ^ (row & 7)) << 4); }
-// LDS byte offset of 16-byte chunk `ch` (0..3) of V row (channel) `row` (0..127): rows of 64 bytes.
-__device__ __forceinline__ int v_lds_off(int row, int ch) {
-  return TILE_BYTES + row * 64 + ((ch ^ ((row >> 1) & 3)) << 4);
-}
+// LDS stage: K tile of 64 rows x 128 bytes with rows padded to 144 bytes, then the V block of 128 rows
+// (channels) x 64 bytes with rows padded to 80 bytes. Row strides of 9 and 5 sixteen-byte units are odd, so the
+// 16 lanes an LDS b128 access serves at a time (16 consecutive rows, same chunk) hit 16 distinct bank groups,
+// and every fragment address is a per-lane base plus a compile-time offset.
+constexpr int K_ROW = 144, V_ROW = 80;
+constexpr int K_LDS = KB * K_ROW;              // 9216
+constexpr int V_LDS = D * V_ROW;               // 10240
+constexpr int STAGE_BYTES = K_LDS + V_LDS;     // 19456
+constexpr int S_MASKED = (int)0xFF800000;      // bits of -inf: the int max ignores it, exp2 gives 0
+__device__ __forceinline__ int k_lds_off(int row, int ch) { return row * K_ROW + (ch << 4); }
+__device__ __forceinline__ int v_lds_off(int row, int ch) { return K_LDS + row * V_ROW + (ch << 4); }
 
-// S^T tile pair for 64 keys x 32 queries of this wave: acc[mt] covers keys 32 mt .. 32 mt + 31.
-__device__ __forceinline__ void qk_tile(const uint8_t* sk, const v4i* qf, int lq, int g, v16i* acc, int init) {
+// S^T tile pair for 64 keys x 32 queries of this wave: acc[mt] covers keys 32 mt .. 32 mt + 31. `init` is the
+// accumulator start value, a loop-invariant register tile (no per-block moves).
+__device__ __forceinline__ void qk_tile(const uint8_t* sk, const v4i* qf, int lq, int g, v16i* acc, const v16i& init) {
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
-    v16i c;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) c[i] = init;
     const int row = 32 * mt + lq;
+    v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + k_lds_off(row, 4 * g)), qf[0], init, 0, 0, 0);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 1; kk < 4; ++kk) {
       const v4i kf = *(const v4i*)(sk + k_lds_off(row, 4 * g + kk));
       c = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[kk], c, 0, 0, 0);
     }
@@ -74,23 +77,24 @@ __device__ __forceinline__ void qk_tile(const uint8_t* sk, const v4i* qf, int lq
 }
 
 // max / sum of a value over the two lane halves (lanes l and l ^ 32 hold the same query)
-__device__ __forceinline__ float halves_max(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+__device__ __forceinline__ int halves_max_i(int x) {
+  auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+  return max((int)r[0], (int)r[1]);
 }
 __device__ __forceinline__ float halves_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ float max32(const float* f) {
-  float a[11];
+// max of 32 ints as a tree of 3-input maxes (v_max3_i32)
+__device__ __forceinline__ int max32i(const int* f) {
+  int a[11];
 #pragma unroll
-  for (int i = 0; i < 10; ++i) a[i] = fmaxf(fmaxf(f[3 * i], f[3 * i + 1]), f[3 * i + 2]);
-  a[10] = fmaxf(f[30], f[31]);
-  const float b0 = fmaxf(fmaxf(a[0], a[1]), a[2]), b1 = fmaxf(fmaxf(a[3], a[4]), a[5]);
-  const float b2 = fmaxf(fmaxf(a[6], a[7]), a[8]), b3 = fmaxf(a[9], a[10]);
-  return fmaxf(fmaxf(b0, b1), fmaxf(b2, b3));
+  for (int i = 0; i < 10; ++i) a[i] = max(max(f[3 * i], f[3 * i + 1]), f[3 * i + 2]);
+  a[10] = max(f[30], f[31]);
+  const int b0 = max(max(a[0], a[1]), a[2]), b1 = max(max(a[3], a[4]), a[5]);
+  const int b2 = max(max(a[6], a[7]), a[8]), b3 = max(a[9], a[10]);
+  return max(max(b0, b1), max(b2, b3));
 }
 
 __device__ __forceinline__ float sum32(const float* p) {
@@ -106,7 +110,7 @@ __device__ __forceinline__ float sum32(const float* p) {
 
 struct Piece {      // online-softmax state of one wave after a range of key blocks
   v16f o[4];        // O^T accumulator, units of the last chunk's V scale
-  float m, l;       // running max (log2 domain, bias included) and row sum (both lane halves combined)
+  float m, l;       // reference max (log2 domain, bias included) and row sum (both lane halves combined)
   int c_last;       // chunk of the last block processed
 };
 
@@ -115,7 +119,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
                                              const float* __restrict__ q_scale, const float* __restrict__ bias,
                                              const int8_t* __restrict__ k8, const float* __restrict__ k_scale,
                                              const uint8_t* __restrict__ v8, const float* __restrict__ v_scale,
-                                             uint8_t (*smem)[2 * TILE_BYTES], int bh, int64_t q0, int j0, int j1,
+                                             uint8_t (*smem)[STAGE_BYTES], int bh, int64_t q0, int j0, int j1,
                                              Piece& st) {
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
   v4i qf[4];
@@ -129,7 +133,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) st.o[mt][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_ref = -INFINITY, l_run = 0.f;
+  v16i magic;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) magic[i] = S_MAGIC;
 
   // chunk and chunk-relative block of j0
   int c = 0;
@@ -137,75 +144,98 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int blk = j0 - a.seg_blk0[c];
   const bool multi = a.n_seg > 1;
 
+  // loader: chunk lc, block lb, uniform base pointers of the block to load next
+  int lc = c, lb = blk;
+  const int8_t* kbase;
+  const uint8_t* vbase;
+  const float* ksbase;
+  auto seek = [&](int cc, int bb) {
+    const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
+    kbase = k8 + (sbh * a.cap + (int64_t)bb * KB) * D;
+    vbase = v8 + (sbh * a.nbc + bb) * TILE_BYTES;
+    ksbase = k_scale + sbh * a.nbc + bb;
+  };
+  seek(lc, lb);
   v4i pk0, pk1, pv0, pv1;
   float ks_next = 0.f;
-  auto gload = [&](int cc, int bb) {
-    const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
-    const int8_t* kp = k8 + (sbh * a.cap + (int64_t)bb * KB) * D;
-    const uint8_t* vp = v8 + (sbh * a.nbc + bb) * TILE_BYTES;
-    pk0 = *(const v4i*)(kp + t * 16);
-    pk1 = *(const v4i*)(kp + 4096 + t * 16);
-    pv0 = *(const v4i*)(vp + t * 16);
-    pv1 = *(const v4i*)(vp + 4096 + t * 16);
-    ks_next = k_scale[sbh * a.nbc + bb];
+  auto gload = [&]() {
+    pk0 = *(const v4i*)(kbase + t * 16);
+    pk1 = *(const v4i*)(kbase + 4096 + t * 16);
+    pv0 = *(const v4i*)(vbase + t * 16);
+    pv1 = *(const v4i*)(vbase + 4096 + t * 16);
+    ks_next = *ksbase;
   };
+  auto advance = [&]() {
+    if (++lb * KB >= a.seg_len[lc]) {
+      ++lc;
+      lb = 0;
+      if (lc < a.n_seg) seek(lc, 0);
+    } else {
+      kbase += TILE_BYTES;
+      vbase += TILE_BYTES;
+      ksbase += 1;
+    }
+  };
+  // per-lane LDS offsets of this thread's stores (thread t: K chunk t and t + 256, V chunk t and t + 256)
+  const int ks_off = k_lds_off(t >> 3, t & 7), vs_off = v_lds_off(t >> 2, t & 3);
   auto lstore = [&](uint8_t* s) {
-    const int id0 = t, id1 = t + 256;
-    *(v4i*)(s + k_lds_off(id0 >> 3, id0 & 7)) = pk0;
-    *(v4i*)(s + k_lds_off(id1 >> 3, id1 & 7)) = pk1;
-    *(v4i*)(s + v_lds_off(id0 >> 2, id0 & 3)) = pv0;
-    *(v4i*)(s + v_lds_off(id1 >> 2, id1 & 3)) = pv1;
+    *(v4i*)(s + ks_off) = pk0;
+    *(v4i*)(s + ks_off + 32 * K_ROW) = pk1;
+    *(v4i*)(s + vs_off) = pv0;
+    *(v4i*)(s + vs_off + 64 * V_ROW) = pv1;
   };
 
   float beta = multi ? bias[((int64_t)c * a.bh + bh) * a.lp + q0 + lq] * a.sl2 : 0.f;
-  gload(c, blk);
+  gload();
+  advance();
   float ks = ks_next;
   lstore(smem[0]);
   __syncthreads();
   int buf = 0;
 
   for (int j = j0; j < j1; ++j) {
-    int cn = c, bn = blk + 1;
-    if (j + 1 >= a.seg_blk0[c + 1]) { cn = c + 1; bn = 0; }
     const bool more = j + 1 < j1;
-    if (more) gload(cn, bn);
+    const int cn = lc, bn = lb;   // the block loaded now is the next one computed
+    if (more) {
+      gload();
+      advance();
+    }
 
     const uint8_t* sk = smem[buf];
     v16i acc[2];
-    qk_tile(sk, qf, lq, g, acc, S_MAGIC);
+    qk_tile(sk, qf, lq, g, acc, magic);
 
     const float cb = qs_sl2 * ks;
-    float f[32];
+    int si[32];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) f[16 * mt + i] = __int_as_float(acc[mt][i]);
+      for (int i = 0; i < 16; ++i) si[16 * mt + i] = acc[mt][i];
     const int valid = a.seg_len[c] - blk * KB;   // keys of this block that exist (>= 1)
     if (valid < KB) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
-          if (key >= valid) f[16 * mt + i] = -INFINITY;
-        }
+      const int vt = valid - 4 * g;   // key 32 mt + 8 (i >> 2) + 4 g + (i & 3) is past the end iff its
+#pragma unroll                        // lane-independent part reaches vt
+      for (int i = 0; i < 32; ++i)
+        if (32 * (i >> 4) + 8 * ((i >> 2) & 3) + (i & 3) >= vt) si[i] = S_MASKED;
     }
-    const float mx = halves_max(max32(f));
-    const float m_blk = (mx - S_MAGIC_F) * cb + beta;
-    const float m_new = fmaxf(m_run, m_blk);
-    if (__any(m_new > m_run)) {   // wave-uniform: rescale only when some row's max moved
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    // reference max: moves only when this block's max exceeds it by more than RESCALE_SLACK
+    const int mx = halves_max_i(max32i(si));
+    const float m_blk = (__int_as_float(mx) - S_MAGIC_F) * cb + beta;
+    const bool moved = m_blk > m_ref + RESCALE_SLACK;
+    if (__any(moved)) {   // wave-uniform and rare
+      const float m_new = moved ? m_blk : m_ref;
+      const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
       l_run *= alpha;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) st.o[mt][i] *= alpha;
-      m_run = m_new;
+      m_ref = m_new;
     }
-    const float kc = (beta - m_run + P_OFFSET) - S_MAGIC_F * cb;
+    const float kc = (beta - m_ref + (P_OFFSET - RESCALE_SLACK)) - S_MAGIC_F * cb;
     float p[32];
 #pragma unroll
-    for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(f[i], cb, kc));
+    for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(si[i]), cb, kc));
     l_run += sum32(p);
     // P^T B operand: byte 16 mt' + 4 i + j of this lane = p[16 mt' + 4 i + j] (keys 32 mt' + 8 i + 4 g + j).
     v8i pb;
@@ -245,7 +275,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     ks = ks_next;
     buf ^= 1;
   }
-  st.m = m_run;
+  st.m = m_ref;
   st.l = halves_sum(l_run);
   st.c_last = c;
 }
@@ -305,7 +335,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restri
                                                           const float* __restrict__ v_scale,
                                                           uint16_t* __restrict__ out, float* __restrict__ o_part,
                                                           float* __restrict__ ml_part, AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2 * TILE_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][STAGE_BYTES];
   const int gid = blockIdx.x, x = gid % XCDS, i = gid / XCDS;
   const int w = threadIdx.x >> 6;
   const XcdPlan p = xcd_plan(a, x);
@@ -399,7 +429,7 @@ __global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict
                                                         const int8_t* __restrict__ k8, int64_t lp,
                                                         int64_t cap, int64_t bh_count, int64_t slot,
                                                         int32_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * TILE_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[K_LDS];
   const int tile = blockIdx.x, blk = blockIdx.y, bh = blockIdx.z;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, lq = lane & 31, g = lane >> 5;
   const int64_t q0 = (int64_t)tile * QT + w * 32;
@@ -408,12 +438,14 @@ __global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) qf[kk] = *(const v4i*)(qrow + 16 * kk);
   const int8_t* kp = k8 + ((slot * bh_count + bh) * cap + (int64_t)blk * KB) * D;
-  const int id0 = t, id1 = t + 256;
-  *(v4i*)(smem + k_lds_off(id0 >> 3, id0 & 7)) = *(const v4i*)(kp + id0 * 16);
-  *(v4i*)(smem + k_lds_off(id1 >> 3, id1 & 7)) = *(const v4i*)(kp + id1 * 16);
+  *(v4i*)(smem + k_lds_off(t >> 3, t & 7)) = *(const v4i*)(kp + t * 16);
+  *(v4i*)(smem + k_lds_off((t >> 3) + 32, t & 7)) = *(const v4i*)(kp + 4096 + t * 16);
   __syncthreads();
+  v16i zero;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zero[i] = 0;
   v16i acc[2];
-  qk_tile(smem, qf, lq, g, acc, 0);
+  qk_tile(smem, qf, lq, g, acc, zero);
   int32_t* op = out + ((int64_t)bh * lp + q0 + lq) * cap + (int64_t)blk * KB;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)

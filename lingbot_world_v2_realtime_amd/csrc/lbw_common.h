@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <climits>
 
 #include "../../include/lbw_attn.h"
 
@@ -16,10 +17,13 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int D = LBW_HEAD_DIM;   // head dim
 constexpr int KB = 64;            // keys per K scale block / V block
 constexpr int QG = 32;            // query rows per Q scale
-constexpr int QT = 128;           // query rows per tile (Lq padding)
+constexpr int QT = 128;           // Lq is padded to whole tiles of this many rows (the attention tile)
 constexpr float V_MAX = 448.f;
 constexpr float AMAX_FLOOR = 1e-7f;
 constexpr float P_OFFSET = 8.807f;           // log2(448): P = exp2(s - m + P_OFFSET) <= 448
+// A row's reference max m moves only when a block's max exceeds it by more than RESCALE_SLACK (log2 units);
+// P = exp2(s - m + P_OFFSET - RESCALE_SLACK) then stays <= 448 and the O rescale is rare.
+constexpr float RESCALE_SLACK = 2.f;
 constexpr int S_MAGIC = 0x4B400000;          // int bits of 12582912.0f = 1.5 * 2^23
 constexpr float S_MAGIC_F = 12582912.f;      // float(S_MAGIC + s) == 12582912 + s for |s| < 2^22
 

@@ -39,12 +39,13 @@ import numpy as np
 import torch
 
 Q_GROUP = 32            # query rows per Q scale
-Q_TILE = 128            # Lq is padded to whole tiles of this many rows
+Q_TILE = 128            # Lq is padded to whole tiles of this many rows (the attention tile)
 K_BLOCK = 64            # keys per K scale and per V block
 HEAD_DIM = 128
 V_MAX = 448.0           # e4m3 max; the V scale maps amax to it
 AMAX_FLOOR = 1e-7
 P_OFFSET = 8.807        # log2(448): P = exp2(s - m + P_OFFSET) <= 448
+RESCALE_SLACK = 2.0     # tau: a row's reference max moves only when a block max exceeds it by more than tau
 LOG2E = 1.4426950408889634
 
 
@@ -225,9 +226,10 @@ def attn_schedule(n_tiles, nb, gx):
     return pieces
 
 
-def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2):
+def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=None):
     """Online softmax over tile-relative key blocks [j0, j1) (numbered across the chunks in order) for the
-    query rows `qf` (q8 as fp32) -> (o in units of the last chunk's V scale, m, l, last chunk index)."""
+    query rows `qf` (q8 as fp32) -> (o in units of the last chunk's V scale, m, l, last chunk index).
+    The reference max m of a row moves only when a block's max exceeds it by more than `tau`."""
     rows, d = qf.shape[0], qf.shape[1]
     m_run = torch.full((rows,), float("-inf"))
     l_run = torch.zeros(rows)
@@ -248,12 +250,14 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2):
             s_int = torch.matmul(qf, c["k8"][hh, k0:k1].float().t())
             cb = (qsr * sl2) * c["k_scale"][hh, b]
             m_blk = s_int.amax(dim=1) * cb + beta
-            m_new = torch.maximum(m_run, m_blk)
+            m_new = torch.where(m_blk > m_run + tau, m_blk, m_run)
+            if stats is not None:
+                stats.append(float((m_new != m_run).float().mean()))
             alpha = torch.exp2(m_run - m_new)
             m_run = m_new
             o = o * alpha[:, None]
             l_run = l_run * alpha
-            kc = (beta - m_new + P_OFFSET).double()
+            kc = (beta - m_new + (P_OFFSET - tau)).double()
             x = (s_int.double() * cb.double()[:, None] + kc[:, None]).float()
             p = torch.exp2(x)
             l_run = l_run + p.sum(dim=1)
@@ -263,11 +267,12 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2):
     return o, m_run, l_run, c_last
 
 
-def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None):
+def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None, stats=None):
     """Emulated quantized attention of q bf16 [Lq, H, D] over quantised chunks (dicts from `requant`), in the
-    kernel's own order: chunks in sequence, 64-key blocks in sequence, a running row max m, and per block
-      m_new = max(m, max_j S_ij * cb + beta),  alpha = exp2(m - m_new),  o = alpha * o,  l = alpha * l,
-      P_ij = exp2(S_ij * cb + beta - m_new + 8.807)  (<= 448),  l += sum P,  o += e4m3(P) . V8,
+    kernel's own order: chunks in sequence, 64-key blocks in sequence, a reference row max m, and per block
+      b = max_j S_ij * cb + beta,  m_new = b if b > m + tau else m,  alpha = exp2(m - m_new),
+      o = alpha * o,  l = alpha * l,  P_ij = exp2(S_ij * cb + beta - m_new + 8.807 - tau)  (<= 448),
+      l += sum P,  o += e4m3(P) . V8,
     with cb = q_scale * k_scale * sm_scale * log2(e); at a chunk boundary o is rescaled by
     v_scale_old / v_scale_new per channel; finally out = o * v_scale / l.
     With `schedule_gx` (the kernel's workgroups per XCD), tiles the kernel splits between workgroups are
@@ -276,6 +281,7 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None):
     """
     q = _as_lhd(q)
     lq, h, d = q.shape
+    tau = RESCALE_SLACK if tau is None else tau
     sl2 = _sl2(sm_scale, d)
     q8, qs = quant_q(q)
     multi = len(chunks) > 1
@@ -310,12 +316,12 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None):
             qsr = qsr_all[hh, a:e]
             beta_of = (lambda ci: bias[ci][hh, a:e]) if multi else (lambda ci: torch.zeros(e - a))
             if t is None:
-                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, 0, nb, sl2)
+                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, 0, nb, sl2, tau, stats)
                 out[a:e, hh] = (o * chunks[cl]["v_scale"][hh][None, :]) * (1.0 / l)[:, None]
                 continue
             parts = []
             for j0, j1 in sched[hh * q_tiles + t]:
-                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2)
+                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats)
                 parts.append((o * chunks[cl]["v_scale"][hh][None, :], m, l))
             mmax = torch.stack([pm for _, pm, _ in parts]).amax(dim=0)
             num = torch.zeros(e - a, d)
