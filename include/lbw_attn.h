@@ -22,7 +22,9 @@
  *   k_scale fp32  [layers][slots][BH][nb]             amax / 127 of each 64-token block
  *   km      fp32  [layers][slots][BH][128]            per-(head, channel) chunk mean (a bf16 value)
  *   v8      uint8 [layers][slots][BH][nb][128][64]    e4m3 V, per 64-key block: [channel][position]
+ *   v8lo    uint8 [layers][slots][BH][nb][128][64]    optional second e4m3 plane: (y - hi) * 16, y = V * 448 / amax
  *   v_scale fp32  [layers][slots][BH][128]            amax / 448 per (head, channel)
+ * With the second plane, V = (hi + lo / 16) * v_scale to about 7 significant bits instead of 4.
  * Position p of a 64-key V block holds key 32*((p&31)>>4) + 8*((p>>2)&3) + 4*(p>>5) + (p&3).
  *
  * Quantised Q (per call): q8 int8 [BH][Lp][128], q_scale fp32 [BH][Lp/32], Lp = Lq rounded up to 128;
@@ -62,7 +64,7 @@ int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len);
 /*
  * Quantise bf16 K and V chunks of `len` tokens into slot `slot` of `layers` consecutive layer caches:
  * the per-(head, channel) K mean, K - mean as int8 per 64-token block, V as e4m3 with one scale per
- * (head, channel). Replaces sage_kvq.requant_all + write_chunk (experiments/modules/sage_kvq.py:78-98)
+ * (head, channel), plus the residual plane when v8lo is not null. Replaces sage_kvq.requant_all + write_chunk (experiments/modules/sage_kvq.py:78-98)
  * and Sage's per_warp_int8 K part / per_channel_fp8 (lingbot/layers/sage_preq.py:115-124).
  * k/v element (layer l, batch b, token t, head h, channel d) sits at l*s_layer + b*s_batch + t*s_tok
  * + h*s_head + d. `workspace` holds lbw_kv_requant_workspace_bytes() bytes, 16-byte aligned; its
@@ -73,7 +75,7 @@ int lbw_kv_requant(const uint16_t* k, const uint16_t* v,
                    int64_t layers, int64_t batch, int64_t len, int64_t heads,
                    int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok, int64_t k_s_head,
                    int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
-                   int8_t* k8, float* k_scale, float* km, uint8_t* v8, float* v_scale,
+                   int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,
                    int64_t slots, int64_t cap, int64_t slot,
                    void* workspace, void* stream);
 
@@ -93,7 +95,8 @@ int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
  * Quantized attention of Q (from lbw_quant_q) over the chunks seg_slot[0..n_seg) of one layer's cache
  * (pointers already offset to that layer), chunk c holding seg_len[c] valid tokens (1..cap). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the
- * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA, fp32 accumulation, V scale
+ * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA (a second fp8 product with the
+ * residual plane, scaled by 2^-4, when v8lo is not null), fp32 accumulation, V scale
  * and 1 / row sum applied at the end. Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
  * 126-127; experiments/modules/sage_kvq.py:107-110). seg_slot / seg_len are host arrays. `workspace` holds
  * lbw_attn_workspace_bytes() bytes (16-byte aligned); two kernels run: the attention over a persistent grid
@@ -101,8 +104,9 @@ int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
  */
 int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias,
                  int64_t batch, int64_t lq, int64_t heads,
-                 const int8_t* k8, const float* k_scale, const uint8_t* v8, const float* v_scale,
-                 int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
+                 const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
+                 const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                 const int32_t* seg_len,
                  uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
                  float sm_scale, void* workspace, void* stream);
 

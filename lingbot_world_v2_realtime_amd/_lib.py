@@ -13,9 +13,9 @@ SIGNATURES = {
     "lbw_kv_requant_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "lbw_kv_requant": (_i32, [_p, _p, _i64, _i64, _i64, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
-                              _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p]),
+                              _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p]),
     "lbw_quant_q": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p]),
-    "lbw_attn_fwd": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p,
+    "lbw_attn_fwd": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p,
                             _p, _i64, _i64, _i64, _f32, _p, _p]),
     "lbw_attn_workspace_bytes": (_i64, []),
     "lbw_attn_workgroups_per_xcd": (_i32, []),

@@ -55,10 +55,13 @@ __device__ __forceinline__ XcdPlan xcd_plan(const AttnArgs& a, int x) {
 constexpr int K_ROW = 144, V_ROW = 80;
 constexpr int K_LDS = KB * K_ROW;              // 9216
 constexpr int V_LDS = D * V_ROW;               // 10240
-constexpr int STAGE_BYTES = K_LDS + V_LDS;     // 19456
+constexpr int STAGE_BYTES = K_LDS + 2 * V_LDS; // 29696: K, V (hi plane), V (lo plane, when present)
 constexpr int S_MASKED = (int)0xFF800000;      // bits of -inf: the int max ignores it, exp2 gives 0
 __device__ __forceinline__ int k_lds_off(int row, int ch) { return row * K_ROW + (ch << 4); }
 __device__ __forceinline__ int v_lds_off(int row, int ch) { return K_LDS + row * V_ROW + (ch << 4); }
+constexpr int VLO_LDS_OFF = V_LDS;             // the lo plane follows the hi plane: v_lds_off(..) + VLO_LDS_OFF
+constexpr int E8M0_ONE = 0x7F7F7F7F;           // MFMA block scale 1.0 in every byte
+constexpr int E8M0_LO = 0x7B7B7B7B;            // 2^-4: the lo plane carries (y - hi) * 16
 
 // S^T tile pair for 64 keys x 32 queries of this wave: acc[mt] covers keys 32 mt .. 32 mt + 31. `init` is the
 // accumulator start value, a loop-invariant register tile (no per-block moves).
@@ -114,11 +117,13 @@ struct Piece {      // online-softmax state of one wave after a range of key blo
   int c_last;       // chunk of the last block processed
 };
 
-// Key blocks [j0, j1) of one tile for this wave's 32 queries.
+// Key blocks [j0, j1) of one tile for this wave's 32 queries. TWO: V has a second (residual) e4m3 plane.
+template <bool TWO>
 __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __restrict__ q8,
                                              const float* __restrict__ q_scale, const float* __restrict__ bias,
                                              const int8_t* __restrict__ k8, const float* __restrict__ k_scale,
-                                             const uint8_t* __restrict__ v8, const float* __restrict__ v_scale,
+                                             const uint8_t* __restrict__ v8, const uint8_t* __restrict__ v8lo,
+                                             const float* __restrict__ v_scale,
                                              uint8_t (*smem)[STAGE_BYTES], int bh, int64_t q0, int j0, int j1,
                                              Piece& st) {
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
@@ -148,21 +153,27 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int lc = c, lb = blk;
   const int8_t* kbase;
   const uint8_t* vbase;
+  const uint8_t* vlbase;
   const float* ksbase;
   auto seek = [&](int cc, int bb) {
     const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
     kbase = k8 + (sbh * a.cap + (int64_t)bb * KB) * D;
     vbase = v8 + (sbh * a.nbc + bb) * TILE_BYTES;
+    if (TWO) vlbase = v8lo + (sbh * a.nbc + bb) * TILE_BYTES;
     ksbase = k_scale + sbh * a.nbc + bb;
   };
   seek(lc, lb);
-  v4i pk0, pk1, pv0, pv1;
+  v4i pk0, pk1, pv0, pv1, pl0, pl1;
   float ks_next = 0.f;
   auto gload = [&]() {
     pk0 = *(const v4i*)(kbase + t * 16);
     pk1 = *(const v4i*)(kbase + 4096 + t * 16);
     pv0 = *(const v4i*)(vbase + t * 16);
     pv1 = *(const v4i*)(vbase + 4096 + t * 16);
+    if (TWO) {
+      pl0 = *(const v4i*)(vlbase + t * 16);
+      pl1 = *(const v4i*)(vlbase + 4096 + t * 16);
+    }
     ks_next = *ksbase;
   };
   auto advance = [&]() {
@@ -173,6 +184,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     } else {
       kbase += TILE_BYTES;
       vbase += TILE_BYTES;
+      if (TWO) vlbase += TILE_BYTES;
       ksbase += 1;
     }
   };
@@ -183,6 +195,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     *(v4i*)(s + ks_off + 32 * K_ROW) = pk1;
     *(v4i*)(s + vs_off) = pv0;
     *(v4i*)(s + vs_off + 64 * V_ROW) = pv1;
+    if (TWO) {
+      *(v4i*)(s + vs_off + VLO_LDS_OFF) = pl0;
+      *(v4i*)(s + vs_off + VLO_LDS_OFF + 64 * V_ROW) = pl1;
+    }
   };
 
   float beta = multi ? bias[((int64_t)c * a.bh + bh) * a.lp + q0 + lq] * a.sl2 : 0.f;
@@ -252,6 +268,12 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       const v4i hi = *(const v4i*)(sk + v_lds_off(row, 2 * g + 1));
       const v8i vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[mt], 0, 0, 0, 0, 0, 0);
+      if (TWO) {   // residual plane, accumulated with block scale 2^-4
+        const v4i lo2 = *(const v4i*)(sk + v_lds_off(row, 2 * g) + VLO_LDS_OFF);
+        const v4i hi2 = *(const v4i*)(sk + v_lds_off(row, 2 * g + 1) + VLO_LDS_OFF);
+        const v8i vl = {lo2[0], lo2[1], lo2[2], lo2[3], hi2[0], hi2[1], hi2[2], hi2[3]};
+        st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vl, pb, st.o[mt], 0, 0, 0, E8M0_LO, 0, E8M0_ONE);
+      }
     }
 
     if (more) lstore(smem[buf ^ 1]);
@@ -326,12 +348,14 @@ __device__ __forceinline__ void store_part(const AttnArgs& a, const Piece& st, c
   if (g == 0) *(float2*)(ml_part + (slot_idx * QT + row) * 2) = make_float2(st.m, st.l);
 }
 
+template <bool TWO>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restrict__ q8,
                                                           const float* __restrict__ q_scale,
                                                           const float* __restrict__ bias,
                                                           const int8_t* __restrict__ k8,
                                                           const float* __restrict__ k_scale,
                                                           const uint8_t* __restrict__ v8,
+                                                          const uint8_t* __restrict__ v8lo,
                                                           const float* __restrict__ v_scale,
                                                           uint16_t* __restrict__ out, float* __restrict__ o_part,
                                                           float* __restrict__ ml_part, AttnArgs a) {
@@ -344,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restri
   for (int tile = p.t_lo + i; tile < p.ts; tile += a.gx) {
     const int bh = tile / a.q_tiles;
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
-    attend_range(a, q8, q_scale, bias, k8, k_scale, v8, v_scale, smem, bh, q0, 0, a.nb, st);
+    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, smem, bh, q0, 0, a.nb, st);
     store_out(a, st, v_scale, out, bh, q0);
   }
   // this workgroup's piece of the split tiles
@@ -357,7 +381,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restri
     const int j1 = (int)((u1 - u + j0 < a.nb) ? (u1 - u + j0) : a.nb);
     const int bh = tile / a.q_tiles;
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
-    attend_range(a, q8, q_scale, bias, k8, k_scale, v8, v_scale, smem, bh, q0, j0, j1, st);
+    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, smem, bh, q0, j0, j1, st);
     if (j0 == 0 && j1 == a.nb) {
       store_out(a, st, v_scale, out, bh, q0);
     } else {
@@ -479,8 +503,8 @@ extern "C" int64_t lbw_attn_workspace_bytes(void) {
 
 extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
                             int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
-                            const uint8_t* v8, const float* v_scale, int64_t slots, int64_t cap, int n_seg,
-                            const int32_t* seg_slot, const int32_t* seg_len, uint16_t* out,
+                            const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
+                            int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len, uint16_t* out,
                             int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head, float sm_scale,
                             void* workspace, void* stream) {
   if (!q8 || !q_scale || !k8 || !k_scale || !v8 || !v_scale || !out || !seg_slot || !seg_len || !workspace)
@@ -490,7 +514,8 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   if (n_seg < 1 || n_seg > LBW_MAX_SEGMENTS) return LBW_E_SEGMENTS;
   if (n_seg > 1 && !bias) return LBW_E_NULL;
   if (o_s_batch % 4 || o_s_tok % 4 || o_s_head % 4) return LBW_E_ALIGN;
-  if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)workspace) & 15 || ((uintptr_t)out & 7))
+  if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo | (uintptr_t)workspace) & 15 ||
+      ((uintptr_t)out & 7))
     return LBW_E_ALIGN;
   AttnArgs a;
   a.lq = lq;
@@ -521,8 +546,12 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   float* o_part = (float*)workspace;
   float* ml_part = o_part + (int64_t)XCDS * a.gx * 2 * QT * D;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(XCDS * a.gx)), dim3(256), 0, st, q8, q_scale, bias, k8,
-                     k_scale, v8, v_scale, out, o_part, ml_part, a);
+  if (v8lo)
+    hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3((unsigned)(XCDS * a.gx)), dim3(256), 0, st, q8, q_scale, bias,
+                       k8, k_scale, v8, v8lo, v_scale, out, o_part, ml_part, a);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3((unsigned)(XCDS * a.gx)), dim3(256), 0, st, q8, q_scale, bias,
+                       k8, k_scale, v8, v8lo, v_scale, out, o_part, ml_part, a);
   hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)a.n_tiles), dim3(256), 0, st, o_part, ml_part, out, a);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;

@@ -3,8 +3,9 @@
 // Three launches, all over (64-token block, batch*head, layer):
 //   1. kv_stats:    per block, fp32 column sums of K and column max |V| (read K and V once).
 //   2. kv_finalize: per (layer, bh, channel), sum the block sums left to right, mean -> bf16, V scale.
-//   3. kv_quant:    K - mean -> int8 per 64-token block; V * (448 / amax) -> e4m3 in the permuted block
-//                   layout (read K and V a second time; a layer's 37 MB is normally still in the MALL).
+//   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * (448 / amax) -> e4m3 hi = rn(y) and, when a
+//                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K
+//                   and V a second time; a layer's 37 MB is normally still in the MALL).
 // The column-sum order is fixed (see the oracle's chunk_mean): s = x[rg] + x[rg+16] + x[rg+32] + x[rg+48]
 // per thread, then rg = 0..15 left to right per block, then the blocks left to right, so the mean is the
 // same bits on every run and on the CPU.
@@ -101,8 +102,8 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
                                                        const float* __restrict__ v_recip,
                                                        int8_t* __restrict__ k8, float* __restrict__ k_scale,
                                                        const float* __restrict__ km,
-                                                       uint8_t* __restrict__ v8) {
-  __shared__ uint32_t s_v[D * 16];   // [channel][16 dwords], dword index xor-swizzled by channel >> 3
+                                                       uint8_t* __restrict__ v8, uint8_t* __restrict__ v8lo) {
+  __shared__ uint32_t s_v[2][D * 16];   // hi / lo planes: [channel][16 dwords], dword xor-swizzled by channel >> 3
   __shared__ float s_red[4];
   const int blk = blockIdx.x, bh = blockIdx.y, layer = blockIdx.z;
   const int t = threadIdx.x, cg = t & 15, kq = t >> 4;
@@ -118,9 +119,9 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
     for (int c = 0; c < 8; ++c) { mean[c] = kmp[c]; vrec[c] = vrp[c]; }
   }
   float x[4][8];
-  uint32_t vb[8];   // per channel: 4 e4m3 bytes of keys 4kq .. 4kq+3
+  uint32_t vb[8], vl[8];   // per channel: 4 e4m3 bytes (hi, lo) of keys 4kq .. 4kq+3
 #pragma unroll
-  for (int c = 0; c < 8; ++c) vb[c] = 0;
+  for (int c = 0; c < 8; ++c) { vb[c] = 0; vl[c] = 0; }
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -140,9 +141,15 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
     for (int c = 0; c < 8; c += 2) {
       float y0 = fminf(fmaxf(__fmul_rn(vf[c], vrec[c]), -V_MAX), V_MAX);
       float y1 = fminf(fmaxf(__fmul_rn(vf[c + 1], vrec[c + 1]), -V_MAX), V_MAX);
-      const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-      vb[c] |= (pk & 0xFFu) << (8 * j);
-      vb[c + 1] |= ((pk >> 8) & 0xFFu) << (8 * j);
+      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+      vb[c] |= ((uint32_t)pk & 0xFFu) << (8 * j);
+      vb[c + 1] |= (((uint32_t)pk >> 8) & 0xFFu) << (8 * j);
+      // residual plane: (y - hi) * 16 is exact in fp32 and within the e4m3 range
+      const float r0 = __fmul_rn(__fsub_rn(y0, __builtin_amdgcn_cvt_f32_fp8(pk, 0)), V_LO_SCALE);
+      const float r1 = __fmul_rn(__fsub_rn(y1, __builtin_amdgcn_cvt_f32_fp8(pk, 1)), V_LO_SCALE);
+      const uint32_t pl = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false);
+      vl[c] |= (pl & 0xFFu) << (8 * j);
+      vl[c + 1] |= ((pl >> 8) & 0xFFu) << (8 * j);
     }
   }
   // block amax over 64 tokens x 128 channels
@@ -153,7 +160,8 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
     const int ch = cg * 8 + c;
-    s_v[ch * 16 + (pdw ^ (ch >> 3))] = vb[c];
+    s_v[0][ch * 16 + (pdw ^ (ch >> 3))] = vb[c];
+    s_v[1][ch * 16 + (pdw ^ (ch >> 3))] = vl[c];
   }
   __syncthreads();
   amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
@@ -171,13 +179,13 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
     }
     *(uint2*)(kout + (kq * 4 + j) * D) = make_uint2(lo, hi);
   }
-  // V tile out: thread t writes 32 contiguous bytes (channel t >> 1, positions 32 * (t & 1) ..)
-  {
+  // V tiles out: thread t writes 32 contiguous bytes (channel t >> 1, positions 32 * (t & 1) ..) of each plane
+  for (int pl = 0; pl < (v8lo ? 2 : 1); ++pl) {
     const int ch = t >> 1, d0 = (t & 1) * 8;
     uint32_t w[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = s_v[ch * 16 + ((d0 + i) ^ (ch >> 3))];
-    uint8_t* vout = v8 + (slot_bh * a.nbc + blk) * (D * KB) + ch * KB + d0 * 4;
+    for (int i = 0; i < 8; ++i) w[i] = s_v[pl][ch * 16 + ((d0 + i) ^ (ch >> 3))];
+    uint8_t* vout = (pl ? v8lo : v8) + (slot_bh * a.nbc + blk) * (D * KB) + ch * KB + d0 * 4;
     *(v4i*)vout = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     *(v4i*)(vout + 16) = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
   }
@@ -197,8 +205,8 @@ extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t laye
                               int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch,
                               int64_t k_s_tok, int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch,
                               int64_t v_s_tok, int64_t v_s_head, int8_t* k8, float* k_scale, float* km,
-                              uint8_t* v8, float* v_scale, int64_t slots, int64_t cap, int64_t slot,
-                              void* workspace, void* stream) {
+                              uint8_t* v8, uint8_t* v8lo, float* v_scale, int64_t slots, int64_t cap,
+                              int64_t slot, void* workspace, void* stream) {
   if (!k || !v || !k8 || !k_scale || !km || !v8 || !v_scale || !workspace) return LBW_E_NULL;
   if (layers <= 0 || batch <= 0 || heads <= 0 || len <= 0 || slots <= 0 || cap <= 0) return LBW_E_SHAPE;
   if (cap % KB != 0 || len > cap || slot < 0 || slot >= slots) return LBW_E_SHAPE;
@@ -206,7 +214,8 @@ extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t laye
   const int64_t strides[8] = {k_s_layer, k_s_batch, k_s_tok, k_s_head, v_s_layer, v_s_batch, v_s_tok, v_s_head};
   for (int64_t s : strides)
     if (s % 8 != 0) return LBW_E_ALIGN;
-  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)workspace) & 15) return LBW_E_ALIGN;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo | (uintptr_t)workspace) & 15)
+    return LBW_E_ALIGN;
   ReqArgs a;
   a.len = len; a.heads = heads; a.bh = batch * heads; a.slots = slots; a.cap = cap; a.slot = slot;
   a.nb = (len + KB - 1) / KB;
@@ -221,7 +230,7 @@ extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t laye
   hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
   hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers), dim3(128), 0, st, a,
                      part_sum, part_amax, v_recip, km, v_scale);
-  hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8);
+  hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }

@@ -19,6 +19,7 @@ constexpr int KB = 64;            // keys per K scale block / V block
 constexpr int QG = 32;            // query rows per Q scale
 constexpr int QT = 128;           // Lq is padded to whole tiles of this many rows (the attention tile)
 constexpr float V_MAX = 448.f;
+constexpr float V_LO_SCALE = 16.f;           // second e4m3 V plane: the residual of the first, times 16
 constexpr float AMAX_FLOOR = 1e-7f;
 constexpr float P_OFFSET = 8.807f;           // log2(448): P = exp2(s - m + P_OFFSET) <= 448
 // A row's reference max m moves only when a block's max exceeds it by more than RESCALE_SLACK (log2 units);

@@ -39,10 +39,11 @@ class RingCache:
     """Quantised K/V ring for `layers` layers x `slots` chunk slots of capacity `cap` tokens (a multiple of 64).
 
     Device layout (include/lbw_attn.h): k8 int8 [L, S, BH, cap, 128]; k_scale fp32 [L, S, BH, cap/64];
-    km fp32 [L, S, BH, 128]; v8 uint8 [L, S, BH, cap/64, 128, 64]; v_scale fp32 [L, S, BH, 128].
+    km fp32 [L, S, BH, 128]; v8 (and, with v_terms=2, the residual plane v8lo) uint8 [L, S, BH, cap/64, 128, 64];
+    v_scale fp32 [L, S, BH, 128].
     """
 
-    def __init__(self, layers, batch, heads, cap, slots, device):
+    def __init__(self, layers, batch, heads, cap, slots, device, v_terms=2):
         if cap % K_BLOCK:
             raise ValueError("cap must be a multiple of 64")
         self.layers, self.batch, self.heads, self.cap, self.slots = layers, batch, heads, cap, slots
@@ -51,7 +52,11 @@ class RingCache:
         self.k8 = torch.zeros(layers, slots, bh, cap, HEAD_DIM, dtype=torch.int8, device=dev)
         self.k_scale = torch.zeros(layers, slots, bh, nb, dtype=torch.float32, device=dev)
         self.km = torch.zeros(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
+        if v_terms not in (1, 2):
+            raise ValueError("v_terms must be 1 or 2")
+        self.v_terms = v_terms
         self.v8 = torch.zeros(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev)
+        self.v8lo = torch.zeros_like(self.v8) if v_terms == 2 else None
         self.v_scale = torch.ones(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
         self.device = dev
 
@@ -60,8 +65,9 @@ class RingCache:
         return self.batch * self.heads
 
     def layer_view(self, layer):
-        """(k8, k_scale, km, v8, v_scale) of one layer, for the per-layer entry points."""
-        return (self.k8[layer], self.k_scale[layer], self.km[layer], self.v8[layer], self.v_scale[layer])
+        """(k8, k_scale, km, v8, v8lo or None, v_scale) of one layer, for the per-layer entry points."""
+        return (self.k8[layer], self.k_scale[layer], self.km[layer], self.v8[layer],
+                self.v8lo[layer] if self.v8lo is not None else None, self.v_scale[layer])
 
 
 def requant_workspace(layers, bh, length, device):
@@ -92,7 +98,8 @@ def kv_requant(k, v, ring, slot, layer0=0, workspace=None):
     st = lib.lbw_kv_requant(
         _ptr(k), _ptr(v), nl, b, n, h, ks[0], ks[1], ks[2], ks[3], vs[0], vs[1], vs[2], vs[3],
         _ptr(ring.k8[layer0]), _ptr(ring.k_scale[layer0]), _ptr(ring.km[layer0]), _ptr(ring.v8[layer0]),
-        _ptr(ring.v_scale[layer0]), ring.slots, ring.cap, slot, _ptr(workspace), _stream(k))
+        _ptr(ring.v8lo[layer0]) if ring.v8lo is not None else None, _ptr(ring.v_scale[layer0]),
+        ring.slots, ring.cap, slot, _ptr(workspace), _stream(k))
     _lib.check(st, "lbw_kv_requant")
 
 
@@ -140,13 +147,13 @@ def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_le
         raise ValueError(f"need 1..{MAX_SEGMENTS} chunks with a length each, got {seg_slots} / {seg_lens}")
     _, _, _, o_b, o_t, o_h = _dims(out, layout)
     sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
-    k8, ksc, _, v8, vsc = ring.layer_view(layer)
+    k8, ksc, _, v8, v8lo, vsc = ring.layer_view(layer)
     slot_arr = (ctypes_i32 * n_seg)(*seg_slots)
     len_arr = (ctypes_i32 * n_seg)(*seg_lens)
     if workspace is None:
         workspace = attn_workspace(q8.device)
     st = lib.lbw_attn_fwd(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
-                          _ptr(v8), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr, _ptr(out),
+                          _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr, _ptr(out),
                           o_b, o_t, o_h, sm_scale, _ptr(workspace), _stream(q8))
     _lib.check(st, "lbw_attn_fwd")
     return out

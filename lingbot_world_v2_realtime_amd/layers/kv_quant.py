@@ -19,11 +19,11 @@ __all__ = ["QuantKVRing", "alloc_cache", "save_chunk", "attend"]
 class QuantKVRing:
     """Quantised K/V ring of `slots` chunk slots for each of `num_layers` layers."""
 
-    def __init__(self, num_layers, batch, heads, chunk_len, slots=4, device="cuda"):
+    def __init__(self, num_layers, batch, heads, chunk_len, slots=4, device="cuda", v_terms=2):
         if slots < 2 or slots > kernels.MAX_SEGMENTS:
             raise ValueError(f"slots must be in 2..{kernels.MAX_SEGMENTS}")
         self.cache = kernels.RingCache(num_layers, batch, heads, kernels.pad_to(chunk_len, kernels.K_BLOCK),
-                                       slots, device)
+                                       slots, device, v_terms)
         self.chunk_len = chunk_len
         self.slots = slots
         self.lens = [0] * slots      # valid tokens in each slot (the same for every layer)
@@ -81,9 +81,9 @@ class QuantKVRing:
         self.lens[self.current] = 0
 
 
-def alloc_cache(num_layers, batch, heads, chunk_len, slots=4, device="cuda"):
+def alloc_cache(num_layers, batch, heads, chunk_len, slots=4, device="cuda", v_terms=2):
     """A quantised chunk ring (cf. sage_kvq.alloc_cache, experiments/modules/sage_kvq.py:38-48)."""
-    return QuantKVRing(num_layers, batch, heads, chunk_len, slots, device)
+    return QuantKVRing(num_layers, batch, heads, chunk_len, slots, device, v_terms)
 
 
 def save_chunk(ring, layer, k, v):

@@ -45,6 +45,8 @@ HEAD_DIM = 128
 V_MAX = 448.0           # e4m3 max; the V scale maps amax to it
 AMAX_FLOOR = 1e-7
 P_OFFSET = 8.807        # log2(448): P = exp2(s - m + P_OFFSET) <= 448
+V_TERMS = 2             # e4m3 V terms: hi, and lo = the residual * 16
+V_LO_SCALE = 16.0
 RESCALE_SLACK = 2.0     # tau: a row's reference max moves only when a block max exceeds it by more than tau
 LOG2E = 1.4426950408889634
 
@@ -153,16 +155,24 @@ def v_scale_of(v):
 
 
 def quant_v(v):
-    """v bf16 [L, H, D] -> (v8 uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, v_scale fp32 [H, D])."""
+    """v bf16 [L, H, D] -> (v8, v8lo uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, v_scale fp32 [H, D]).
+
+    Two e4m3 terms: y = v * (448 / amax); hi = e4m3(y); lo = e4m3((y - hi) * 16), so v ~ (hi + lo / 16) * v_scale.
+    y - hi is exact in fp32 (hi is y rounded to 3 mantissa bits) and |y - hi| * 16 <= 256 stays in range."""
     v = _as_lhd(v)
     n, h, d = v.shape
     lp = pad_to(n, K_BLOCK)
     vs, recip = v_scale_of(v)
     y = torch.zeros(h, lp, d, dtype=torch.float32)
     y[:, :n] = v.float().permute(1, 0, 2) * recip[:, None, :]
-    bits = e4m3_encode(y).view(h, lp // K_BLOCK, K_BLOCK, d)       # [h, b, key, d]
-    bits = bits[:, :, torch.from_numpy(V_KEY_OF_POS)]               # [h, b, pos, d]
-    return bits.permute(0, 1, 3, 2).contiguous(), vs
+    y = y.clamp(-V_MAX, V_MAX)
+    hi = e4m3_encode(y)
+    lo = e4m3_encode((y - e4m3_decode(hi)) * V_LO_SCALE)
+    planes = []
+    for bits in (hi, lo):
+        bits = bits.view(h, lp // K_BLOCK, K_BLOCK, d)[:, :, torch.from_numpy(V_KEY_OF_POS)]   # [h, b, pos, d]
+        planes.append(bits.permute(0, 1, 3, 2).contiguous())
+    return planes[0], planes[1], vs
 
 
 def requant(k, v):
@@ -170,16 +180,20 @@ def requant(k, v):
     k = _as_lhd(k)
     km = chunk_mean(k)
     k8, ks = quant_k(k, km)
-    v8, vs = quant_v(v)
-    return {"k8": k8, "k_scale": ks, "km": km, "v8": v8, "v_scale": vs, "n": k.shape[0]}
+    v8, v8lo, vs = quant_v(v)
+    return {"k8": k8, "k_scale": ks, "km": km, "v8": v8, "v8lo": v8lo, "v_scale": vs, "n": k.shape[0]}
 
 
-def dequant_v(chunk):
-    """fp8 V of a quantised chunk back to fp32 [H, n, D] in key order, without the V scale."""
-    v8 = chunk["v8"]                                     # [h, nb, d, 64] positions
-    h, nb, d, _ = v8.shape
-    vals = e4m3_decode(v8)[:, :, :, torch.from_numpy(V_POS_OF_KEY)]   # [h, nb, d, key]
-    return vals.permute(0, 1, 3, 2).reshape(h, nb * K_BLOCK, d)[:, :chunk["n"]]
+def dequant_v(chunk, terms=None):
+    """e4m3 V of a quantised chunk back to fp32 [H, n, D] in key order, without the V scale: hi + lo / 16
+    (or hi alone with terms=1)."""
+    terms = V_TERMS if terms is None else terms
+    h, nb, d, _ = chunk["v8"].shape
+    out = 0
+    for bits, w in ((chunk["v8"], 1.0), (chunk["v8lo"], 1.0 / V_LO_SCALE))[:terms]:
+        vals = e4m3_decode(bits)[:, :, :, torch.from_numpy(V_POS_OF_KEY)]   # [h, nb, d, key]
+        out = out + vals.permute(0, 1, 3, 2).reshape(h, nb * K_BLOCK, d)[:, :chunk["n"]] * w
+    return out
 
 
 def qk_logits(q8, k8):
@@ -418,9 +432,9 @@ def attention_ops(lq, lk, h, d=HEAD_DIM, b=1):
     return 4.0 * b * h * lq * lk * d
 
 
-def requant_bytes(n, h, d=HEAD_DIM):
-    """Algorithmic bytes of one chunk's re-quant: read bf16 K and V once, write int8 K and fp8 V once,
-    plus the per-block K scales and the per-channel mean and V scale."""
+def requant_bytes(n, h, d=HEAD_DIM, v_planes=V_TERMS):
+    """Algorithmic bytes of one chunk's re-quant: read bf16 K and V once, write int8 K and the e4m3 V plane(s)
+    once, plus the per-block K scales and the per-channel mean and V scale."""
     nb = pad_to(n, K_BLOCK) // K_BLOCK
-    return 2 * n * h * d * 2 + 2 * n * h * d + nb * h * 4 + 2 * h * d * 4
+    return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + 2 * h * d * 4
 

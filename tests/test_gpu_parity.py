@@ -30,6 +30,8 @@ def _check_chunk(ring, layer, slot, ref, n, bh_slice=slice(None)):
     torch.testing.assert_close(ring.k_scale[layer, slot, :, :nb].cpu()[bh_slice], ref["k_scale"], rtol=0, atol=0)
     assert torch.equal(ring.k8[layer, slot, :, :nb * 64].cpu()[bh_slice], ref["k8"])
     assert torch.equal(ring.v8[layer, slot, :, :nb].cpu()[bh_slice], ref["v8"])
+    if ring.v8lo is not None:
+        assert torch.equal(ring.v8lo[layer, slot, :, :nb].cpu()[bh_slice], ref["v8lo"])
 
 
 @pytest.mark.parametrize("n", [1, 16, 63, 64, 65, 200, 1508])
