@@ -7,8 +7,8 @@ kernel. The cached chunks are quantised from their own bf16 values before the ti
 
 Reported (one JSON line on stdout):
   value        attention TOPS of the whole call = 4 * H * Lq * Lk * d / step time
-  roofline     the attention kernel alone: algorithmic ops per launch / its HIP-event launch time vs
-               5.0 POPS dense INT8/FP8 MFMA peak
+  roofline     the attention call alone (attn_fwd_kernel and the small merge of split query tiles, one
+               lbw_attn_fwd): algorithmic ops per call / its HIP-event time vs 5.0 POPS dense INT8/FP8 MFMA
   requant      the K/V re-quant of a saved chunk for 30 layers in one call, algorithmic GB/s vs 8 TB/s
   cpu_baseline the torch CPU emulation of the same scheme (oracle/emu.py) on a bounded sample of the call
 """
@@ -32,6 +32,38 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def synthetic_inputs(lq, lk, h=H, d=D, seed=0, mem_chunks=0, chunk_len=None):
+    """Seeded bf16 NHD inputs [1, L, H, D], generated in the order Q, K, K channel offset, V, then K, V of each
+    memory chunk: Q, V ~ N(0, 1); K ~ N(0, 1) + o[h, d], o ~ N(0, 3) (the per-channel offset the K mean
+    smoothing removes); memory chunks ~ N(0, 1.5)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, lq, h, d, generator=g)
+    k = torch.randn(1, lk, h, d, generator=g)
+    off = torch.randn(1, 1, h, d, generator=g) * 3.0
+    v = torch.randn(1, lk, h, d, generator=g)
+    mem = []
+    for _ in range(mem_chunks):
+        n = chunk_len or lk
+        mk = torch.randn(1, n, h, d, generator=g) * 1.5
+        mv = torch.randn(1, n, h, d, generator=g) * 1.5
+        mem.append((mk.to(torch.bfloat16), mv.to(torch.bfloat16)))
+    return q.to(torch.bfloat16), (k + off).to(torch.bfloat16), v.to(torch.bfloat16), mem
+
+
+def attention_ops(lq, lk, h=H, d=D, b=1):
+    """Algorithmic ops of one attention call: QK^T and PV, 2 * Lq * Lk * d each per head (one multiply-add =
+    2 ops), the count the reference's roofline uses (tools/roofline.py:91-95)."""
+    return 4.0 * b * h * lq * lk * d
+
+
+def requant_bytes(n, h=H, d=D, v_planes=2):
+    """Algorithmic bytes of one chunk's K/V re-quant: bf16 K and V read once; int8 K and the e4m3 V plane(s)
+    written once; one fp32 scale per 64-token K block; fp32 mean and V scale per (head, channel)."""
+    nb = (n + 63) // 64
+    return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + 2 * h * d * 4
+
+
 def traffic_from_profiles():
     """HBM bytes per attention launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the
     copy-kernel calibration), committed in profiles/; None when not measured."""
@@ -49,7 +81,7 @@ def cpu_baseline(heads=3, q_rows=LQ):
     from oracle import emu
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    q, k, v, mem = emu.make_inputs(LQ, CHUNK, h=heads, seed=0, mem_chunks=MEM, chunk_len=CHUNK)
+    q, k, v, mem = synthetic_inputs(LQ, CHUNK, h=heads, seed=0, mem_chunks=MEM, chunk_len=CHUNK)
     chunks = [emu.requant(mk, mv) for mk, mv in mem]
     t0 = time.perf_counter()
     cur = emu.requant(k, v)
@@ -57,10 +89,61 @@ def cpu_baseline(heads=3, q_rows=LQ):
     dt = time.perf_counter() - t0
     frac = (q_rows / LQ) * heads / H                      # share of the full call's work in the sample
     full_s = dt / frac
-    ops = emu.attention_ops(LQ, LK, H, D)
+    ops = attention_ops(LQ, LK, H, D)
     return {"value": round(ops / full_s / 1e12, 6), "unit": "TOPS", "cores": cores, "kind": "port",
             "sample": f"{heads} of {H} heads x {q_rows} of {LQ} queries x {LK} keys (torch emulation incl. Q and "
                       f"current-chunk quant), {dt:.2f} s, scaled x{1 / frac:.0f} -> {full_s:.1f} s per call"}
+
+
+def _timed(fn, n, stream):
+    """Mean milliseconds of fn() over n launches, HIP events on `stream`."""
+    import torch
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(n):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def profile_only(args, dev):
+    """One part of the step, alone, for counter runs: the attention call (attn_fwd_kernel + merge) on the
+    cfg-3 ring, the 30-layer K/V re-quant, or a plain copy of known size."""
+    import torch
+    from lingbot_world_v2_realtime_amd import kernels
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    stream = torch.cuda.current_stream(dev)
+    if args.only == "copy":
+        n = 1 << 30                                         # 2^30 bf16 = 2 GiB read + 2 GiB written
+        a = torch.empty(n, dtype=torch.bfloat16, device=dev).normal_()
+        b = torch.empty_like(a)
+        fn = lambda: b.copy_(a)                             # noqa: E731
+        nbytes = 2 * a.numel() * a.element_size()
+    elif args.only == "requant":
+        kl = torch.randn(LAYERS, 1, CHUNK, H, D, device=dev).to(torch.bfloat16)
+        vl = torch.randn(LAYERS, 1, CHUNK, H, D, device=dev).to(torch.bfloat16)
+        rq = QuantKVRing(LAYERS, 1, H, CHUNK, slots=MEM + 1, device=dev)
+        fn = lambda: rq.write_layers(kl, vl)                # noqa: E731
+        nbytes = LAYERS * requant_bytes(CHUNK, H, D)
+    else:
+        q, k, v, mem = synthetic_inputs(LQ, CHUNK, h=H, seed=0, mem_chunks=MEM, chunk_len=CHUNK)
+        ring = QuantKVRing(1, 1, H, CHUNK, slots=MEM + 1, device=dev)
+        for mk, mv in mem:
+            ring.write(0, mk.to(dev), mv.to(dev))
+            ring.commit()
+        ring.write(0, k.to(dev), v.to(dev))
+        slots, lens = ring.attended()
+        q = q.to(dev)
+        q8, qs, bias = kernels.quant_q(q, "NHD", ring.cache, 0, slots)
+        o = torch.empty_like(q)
+        fn = lambda: kernels.attn_fwd(q8, qs, bias, 1, LQ, H, ring.cache, 0, slots, lens, o)  # noqa: E731
+        nbytes = None
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    ms = _timed(fn, args.steps, stream)
+    print(json.dumps({"only": args.only, "launches": args.steps, "ms": round(ms, 4), "bytes": nbytes}), flush=True)
 
 
 def main():
@@ -70,6 +153,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU emulation baseline")
     ap.add_argument("--cpu-heads", type=int, default=3)
+    ap.add_argument("--only", choices=["attn", "requant", "copy"],
+                    help="profiling run: after the set-up, launch only this part --steps times and print its "
+                         "mean time (copy: a 2 GiB device-to-device copy, the byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the attention path shards by head with no communication inside the "
@@ -77,13 +163,14 @@ def main():
         sys.exit(2)
 
     import torch
-    from oracle import emu
     from lingbot_world_v2_realtime_amd import kernels
     from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    q, k, v, mem = emu.make_inputs(LQ, CHUNK, h=H, seed=0, mem_chunks=MEM, chunk_len=CHUNK)
+    if args.only:
+        return profile_only(args, dev)
+    q, k, v, mem = synthetic_inputs(LQ, CHUNK, h=H, seed=0, mem_chunks=MEM, chunk_len=CHUNK)
     q, k, v = q.to(dev), k.to(dev), v.to(dev)
     ring = QuantKVRing(1, 1, H, CHUNK, slots=MEM + 1, device=dev)
     for mk, mv in mem:
@@ -104,7 +191,7 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = wall / args.steps * 1e3
-    ops = emu.attention_ops(LQ, LK, H, D)
+    ops = attention_ops(LQ, LK, H, D)
     tops = ops / (ms_step * 1e-3) / 1e12
 
     # attention kernel alone, HIP events on the stream it is launched on
@@ -114,14 +201,8 @@ def main():
     stream = torch.cuda.current_stream(dev)
     for _ in range(5):
         kernels.attn_fwd(q8, qs, bias, 1, LQ, H, ring.cache, 0, slots, lens, o)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n_k = max(args.steps, 20)
-    e0.record(stream)
-    for _ in range(n_k):
-        kernels.attn_fwd(q8, qs, bias, 1, LQ, H, ring.cache, 0, slots, lens, o)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    attn_ms = e0.elapsed_time(e1) / n_k
+    attn_ms = _timed(lambda: kernels.attn_fwd(q8, qs, bias, 1, LQ, H, ring.cache, 0, slots, lens, o),
+                     max(args.steps, 20), stream)
     attn_tops = ops / (attn_ms * 1e-3) / 1e12
 
     # K/V re-quant, 30 layers in one call (cfg 4)
@@ -130,15 +211,8 @@ def main():
     rq = QuantKVRing(LAYERS, 1, H, CHUNK, slots=MEM + 1, device=dev)
     for _ in range(3):
         rq.write_layers(kl, vl)
-    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n_r = 10
-    r0.record(stream)
-    for _ in range(n_r):
-        rq.write_layers(kl, vl)
-    r1.record(stream)
-    torch.cuda.synchronize()
-    rq_ms = r0.elapsed_time(r1) / n_r
-    rq_bytes = LAYERS * emu.requant_bytes(CHUNK, H, D)
+    rq_ms = _timed(lambda: rq.write_layers(kl, vl), 10, stream)
+    rq_bytes = LAYERS * requant_bytes(CHUNK, H, D)
     rq_gbps = rq_bytes / (rq_ms * 1e-3) / 1e9
     del kl, vl, rq
 
@@ -161,7 +235,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(attn_tops, 2), "peak": MFMA_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tops / MFMA_PEAK_TOPS, 4),
                      "traffic": traffic_from_profiles(),
-                     "kernel": "attn_fwd_kernel", "kernel_ms": round(attn_ms, 4),
+                     "kernel": "lbw_attn_fwd = attn_fwd_kernel + attn_merge_kernel", "kernel_ms": round(attn_ms, 4),
                      "ops_per_launch": ops},
         "requant": {"layers": LAYERS, "ms": round(rq_ms, 4), "bytes": rq_bytes, "GB/s": round(rq_gbps, 1),
                     "frac_hbm": round(rq_gbps / HBM_PEAK_GBPS, 4)},

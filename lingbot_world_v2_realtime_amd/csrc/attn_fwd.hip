@@ -542,6 +542,7 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   a.q_tiles = (int)(a.lp / QT);
   if ((int64_t)a.q_tiles * a.bh > 0x7fffffff / 2) return LBW_E_SHAPE;
   a.n_tiles = (int)(a.q_tiles * a.bh);
+  if (const int dv = check_device()) return dv;
   a.gx = attn_wgs_per_xcd();
   float* o_part = (float*)workspace;
   float* ml_part = o_part + (int64_t)XCDS * a.gx * 2 * QT * D;
@@ -562,6 +563,7 @@ extern "C" int lbw_qk_logits_i32(const int8_t* q8, int64_t bh, int64_t lq, const
   if (!q8 || !k8 || !out) return LBW_E_NULL;
   if (bh <= 0 || bh > 65535 || lq <= 0 || cap <= 0 || cap % KB || slot < 0 || slot >= slots) return LBW_E_SHAPE;
   if (((uintptr_t)q8 | (uintptr_t)k8) & 15) return LBW_E_ALIGN;
+  if (const int dv = check_device()) return dv;
   const int64_t lp = (lq + QT - 1) / QT * QT;
   hipLaunchKernelGGL(qk_logits_kernel, dim3((unsigned)(lp / QT), (unsigned)(cap / KB), (unsigned)bh), dim3(256),
                      0, (hipStream_t)stream, q8, k8, lp, cap, bh, slot, out);

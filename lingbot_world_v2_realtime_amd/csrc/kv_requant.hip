@@ -225,6 +225,7 @@ extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t laye
   float* part_sum = (float*)workspace;
   float* part_amax = part_sum + layers * a.bh * a.nb * D;
   float* v_recip = part_amax + layers * a.bh * a.nb * D;
+  if (const int dv = check_device()) return dv;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
   hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);

@@ -1,4 +1,6 @@
 // Status strings and version of the C-ABI.
+#include <cstring>
+
 #include "lbw_common.h"
 
 extern "C" const char* lbw_status_string(int status) {
@@ -15,3 +17,21 @@ extern "C" const char* lbw_status_string(int status) {
 }
 
 extern "C" int lbw_version(void) { return 100; }
+
+namespace lbw {
+
+// LBW_OK when the current device is a gfx950 (the only target the code objects are built for), else
+// LBW_E_DEVICE; the answer is cached per device ordinal.
+int check_device() {
+  static int cached[64] = {0};   // 0 unknown, 1 gfx950, 2 other
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LBW_E_DEVICE;
+  if (cached[dev] == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return LBW_E_DEVICE;
+    cached[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+  }
+  return cached[dev] == 1 ? LBW_OK : LBW_E_DEVICE;
+}
+
+}  // namespace lbw

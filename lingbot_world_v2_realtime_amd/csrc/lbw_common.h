@@ -66,6 +66,9 @@ __device__ __forceinline__ float wave_max(float x) {
   return x;
 }
 
+// LBW_OK when the current device is a gfx950, else LBW_E_DEVICE (defined in lbw_abi.hip).
+int check_device();
+
 // Position of key k (0..63) inside a 64-key fp8 V block.
 __device__ __forceinline__ int v_pos_of_key(int k) {
   return 32 * ((k >> 2) & 1) + 16 * ((k >> 5) & 1) + 4 * ((k >> 3) & 3) + (k & 3);

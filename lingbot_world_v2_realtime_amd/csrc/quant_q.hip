@@ -87,6 +87,7 @@ extern "C" int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t
     }
   }
   if (a.lp / QG > 0x7fffffff) return LBW_E_SHAPE;
+  if (const int dv = check_device()) return dv;
   hipLaunchKernelGGL(quant_q_kernel, dim3((unsigned)(a.lp / QG), (unsigned)a.bh), dim3(64), 0,
                      (hipStream_t)stream, q, a, q8, q_scale, km, bias);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;

@@ -1,0 +1,148 @@
+"""C-ABI of liblbw_attn.so without a GPU: the library loads, exports every function include/lbw_attn.h declares
+with the argument count the ctypes binding uses, and rejects bad arguments with the documented status codes
+before touching the device."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from lingbot_world_v2_realtime_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(__file__), "..", "include", "lbw_attn.h")
+
+OK, E_NULL, E_SHAPE, E_ALIGN, E_DEVICE, E_LAUNCH, E_SEGMENTS = range(7)
+FAKE = 1 << 20          # a 16-byte aligned non-null address; never dereferenced on the paths tested here
+
+
+def declared_functions():
+    """{name: number of parameters} of every function prototype in the header."""
+    src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:const\s+)?\w+\s*\*?\s*(lbw_\w+)\s*\(([^)]*)\)\s*;", src, flags=re.M):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("liblbw_attn.so is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_header_declarations_are_bound_and_exported(lib):
+    decl = declared_functions()
+    assert len(decl) == 9
+    assert set(decl) == set(_lib.SIGNATURES)
+    for name, n in decl.items():
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+        assert hasattr(lib, name)
+    nm = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in nm.splitlines() if " T " in line and "lbw_" in line}
+    assert set(decl) <= exported
+
+
+def test_status_strings_and_version(lib):
+    names = [lib.lbw_status_string(s).decode() for s in range(7)]
+    assert names[0] == "ok" and len(set(names)) == 7
+    assert lib.lbw_status_string(99).decode() == "unknown status"
+    assert lib.lbw_version() == 100
+
+
+def test_requant_workspace_formula(lib):
+    for layers, bh, n in ((1, 1, 1), (30, 24, 1508), (2, 3, 64), (1, 5, 65)):
+        nb = -(-n // 64)
+        assert lib.lbw_kv_requant_workspace_bytes(layers, bh, n) == (2 * layers * bh * nb * 128 + layers * bh * 128) * 4
+    assert lib.lbw_kv_requant_workspace_bytes(0, 1, 1) == 0
+
+
+def requant(lib, **kw):
+    a = dict(k=FAKE, v=FAKE, layers=1, batch=1, len=100, heads=2, ks=(0, 0, 256, 128), vs=(0, 0, 256, 128),
+             k8=FAKE, k_scale=FAKE, km=FAKE, v8=FAKE, v8lo=None, v_scale=FAKE, slots=4, cap=128, slot=0,
+             ws=FAKE)
+    a.update(kw)
+    return lib.lbw_kv_requant(a["k"], a["v"], a["layers"], a["batch"], a["len"], a["heads"], *a["ks"], *a["vs"],
+                              a["k8"], a["k_scale"], a["km"], a["v8"], a["v8lo"], a["v_scale"], a["slots"],
+                              a["cap"], a["slot"], a["ws"], None)
+
+
+def test_requant_argument_checks(lib):
+    assert requant(lib, k=None) == E_NULL
+    assert requant(lib, ws=None) == E_NULL
+    assert requant(lib, len=0) == E_SHAPE
+    assert requant(lib, len=129) == E_SHAPE            # more tokens than the slot holds
+    assert requant(lib, cap=100) == E_SHAPE            # capacity not a multiple of 64
+    assert requant(lib, slot=4) == E_SHAPE
+    assert requant(lib, batch=300, heads=300) == E_SHAPE
+    assert requant(lib, ks=(0, 0, 256, 129)) == E_ALIGN
+    assert requant(lib, k8=FAKE + 8) == E_ALIGN
+    assert requant(lib, v8lo=FAKE + 4) == E_ALIGN
+
+
+def quant_q(lib, **kw):
+    a = dict(q=FAKE, batch=1, lq=100, heads=2, st=(0, 256, 128), q8=FAKE, qs=FAKE, km=FAKE, slots=4, n_seg=0,
+             seg=None, bias=FAKE)
+    a.update(kw)
+    return lib.lbw_quant_q(a["q"], a["batch"], a["lq"], a["heads"], *a["st"], a["q8"], a["qs"], a["km"],
+                           a["slots"], a["n_seg"], a["seg"], a["bias"], None)
+
+
+def test_quant_q_argument_checks(lib):
+    seg = (ctypes.c_int32 * 2)(0, 5)
+    assert quant_q(lib, q=None) == E_NULL
+    assert quant_q(lib, lq=0) == E_SHAPE
+    assert quant_q(lib, n_seg=9) == E_SEGMENTS
+    assert quant_q(lib, st=(0, 256, 12)) == E_ALIGN
+    assert quant_q(lib, n_seg=2, seg=None) == E_NULL
+    assert quant_q(lib, n_seg=2, seg=seg) == E_SEGMENTS   # slot 5 of a 4-slot cache
+
+
+def attn(lib, **kw):
+    seg = (ctypes.c_int32 * 8)(0, 1, 2, 3, 0, 0, 0, 0)
+    ln = (ctypes.c_int32 * 8)(128, 128, 128, 100, 0, 0, 0, 0)
+    a = dict(q8=FAKE, qs=FAKE, bias=FAKE, batch=1, lq=100, heads=2, k8=FAKE, ks=FAKE, v8=FAKE, v8lo=None,
+             vs=FAKE, slots=4, cap=128, n_seg=4, seg=seg, ln=ln, out=FAKE, os=(0, 256, 128), sm=0.088, ws=FAKE)
+    a.update(kw)
+    return lib.lbw_attn_fwd(a["q8"], a["qs"], a["bias"], a["batch"], a["lq"], a["heads"], a["k8"], a["ks"],
+                            a["v8"], a["v8lo"], a["vs"], a["slots"], a["cap"], a["n_seg"], a["seg"], a["ln"],
+                            a["out"], *a["os"], a["sm"], a["ws"], None)
+
+
+def test_attn_argument_checks(lib):
+    assert attn(lib, q8=None) == E_NULL
+    assert attn(lib, ws=None) == E_NULL
+    assert attn(lib, bias=None) == E_NULL                 # several chunks need the q . mean bias
+    assert attn(lib, cap=96) == E_SHAPE
+    assert attn(lib, sm=0.0) == E_SHAPE
+    assert attn(lib, sm=float("nan")) == E_SHAPE
+    assert attn(lib, n_seg=0) == E_SEGMENTS
+    assert attn(lib, n_seg=9) == E_SEGMENTS
+    assert attn(lib, ln=(ctypes.c_int32 * 8)(128, 129, 1, 1, 0, 0, 0, 0)) == E_SEGMENTS
+    assert attn(lib, ln=(ctypes.c_int32 * 8)(128, 0, 1, 1, 0, 0, 0, 0)) == E_SEGMENTS
+    assert attn(lib, seg=(ctypes.c_int32 * 8)(0, 1, 2, 4, 0, 0, 0, 0)) == E_SEGMENTS
+    assert attn(lib, os=(0, 256, 130)) == E_ALIGN
+    assert attn(lib, out=FAKE + 2) == E_ALIGN
+    assert attn(lib, v8=FAKE + 8) == E_ALIGN
+    assert lib.lbw_qk_logits_i32(FAKE, 2, 100, None, 1, 128, 0, FAKE, None) == E_NULL
+    assert lib.lbw_qk_logits_i32(FAKE, 2, 100, FAKE, 1, 128, 1, FAKE, None) == E_SHAPE
+
+
+def test_valid_call_without_gfx950_is_refused(lib):
+    """With arguments that pass every check, a process that sees no gfx950 device gets LBW_E_DEVICE and no
+    launch. (Only meaningful where no GPU is visible; on a GPU host this path would launch on fake pointers.)"""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    assert requant(lib) == E_DEVICE
+    assert quant_q(lib) == E_DEVICE
+    assert attn(lib) == E_DEVICE
+    assert lib.lbw_qk_logits_i32(FAKE, 2, 100, FAKE, 1, 128, 0, FAKE, None) == E_DEVICE
+
+
+def test_loader_fails_loudly_without_library(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(ImportError):
+        _lib.load(str(tmp_path / "missing.so"))

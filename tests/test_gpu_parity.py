@@ -214,3 +214,17 @@ def test_attention_cfg3_tolerance():
     print(f"cfg3 vs-sdpa max {e.max():.3e} mean {e.mean():.3e} (|out| mean {sd.abs().mean():.3e})")
     assert e.mean() < SDPA_MEAN_ABS
     assert e.max() < SDPA_MAX_ABS
+
+
+def test_reference_cosine_gate():
+    """The reference's attention quality gate (docs/OPTIMIZATIONS.md:782-790): randn Q [1, 6032, 12, 128],
+    K/V [1, 27144, 12, 128] bf16 NHD, cosine against fp32 SDPA; its INT8 kernel measured 0.999246."""
+    g = torch.Generator(device=DEV).manual_seed(0)
+    q, k, v = (torch.randn(1, n, 12, 128, device=DEV, generator=g).to(torch.bfloat16) for n in (6032, 27144, 27144))
+    from lingbot_world_v2_realtime_amd import sage_attention
+    out = sage_attention(q, k, v).float()
+    sd = _sdpa_gpu_fp32(q, k, v)
+    cos = torch.nn.functional.cosine_similarity(out.flatten(), sd.flatten(), dim=0).item()
+    e = (out - sd).abs()
+    print(f"cosine vs fp32 SDPA {cos:.6f} (reference INT8: 0.999246); max {e.max():.3e} mean {e.mean():.3e}")
+    assert cos >= 0.999246

@@ -1,0 +1,265 @@
+"""Pins of the CPU oracle (oracle/emu.py) against the mathematics that fixes it: an independent e4m3 encoder
+written from the format definition, round-half-even ties, closed forms, exact invariances, int64 brute force,
+fp32 softmax attention, and the split-KV merge identity. No GPU needed."""
+import math
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import emu
+
+
+# ---------------------------------------------------------------- e4m3 (OCP fn) from the format definition
+
+def e4m3_ref(x):
+    """Nearest e4m3fn value bits of a Python float |x| <= 448 (ties to even), by enumerating the 256 codes."""
+    best = None
+    for code in range(256):
+        e, m = (code >> 3) & 15, code & 7
+        if e == 15 and m == 7:
+            continue                                   # NaN
+        mag = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+        val = -mag if code & 128 else mag
+        d = abs(val - x)
+        key = (d, m & 1)                               # nearest, then even mantissa
+        if best is None or key < best[0] or (key == best[0] and (code & 128) == (128 if x < 0 else 0)):
+            best = (key, code, val)
+    code = best[1]
+    if best[2] == 0.0:                                 # signed zero follows the input's sign
+        code = 128 if math.copysign(1.0, x) < 0 else 0
+    return code
+
+
+def test_e4m3_encoder_matches_format_definition():
+    rng = np.random.default_rng(0)
+    xs = [0.0, -0.0, 448.0, -448.0, 2.0 ** -9, 2.0 ** -10, 1.5 * 2.0 ** -9, 3 * 2.0 ** -10, 232.0, 240.0, 17.0,
+          0.0174, 1.0625, 1.1875, -3.25]
+    # every e4m3 value and the midpoints between neighbours (the ties), plus random values
+    vals = sorted({emu.e4m3_decode(torch.tensor([c], dtype=torch.uint8)).item() for c in range(256)
+                   if (c & 0x7F) != 0x7F})
+    xs += vals + [(a + b) / 2 for a, b in zip(vals, vals[1:])]
+    xs += list(rng.uniform(-448, 448, 300)) + list(rng.uniform(-0.05, 0.05, 300))
+    x32 = torch.tensor(xs, dtype=torch.float32)
+    got = emu.e4m3_encode(x32).tolist()
+    want = [e4m3_ref(float(v)) for v in x32.tolist()]
+    assert got == want
+
+
+# ---------------------------------------------------------------- int8 quantisers
+
+def test_int8_group_quant_closed_form():
+    torch.manual_seed(1)
+    lq, h = 200, 3
+    # rows of group g scaled by 2^g so a wrong row -> group map changes the scales
+    q = torch.randn(lq, h, 128) * (2.0 ** (torch.arange(lq) // 32).float())[:, None, None]
+    q = q.to(torch.bfloat16)
+    q8, qs = emu.quant_q(q)
+    assert q8.shape == (h, emu.pad_to(lq, emu.Q_TILE), 128) and qs.shape == (h, emu.pad_to(lq, emu.Q_TILE) // 32)
+    x = torch.zeros(h, q8.shape[1], 128)
+    x[:, :lq] = q.float().permute(1, 0, 2)
+    for hh in range(h):
+        for gi in range(qs.shape[1]):
+            blk = x[hh, 32 * gi:32 * gi + 32]
+            amax = max(float(blk.abs().max()), 1e-7)
+            assert qs[hh, gi].item() == np.float32(np.float32(amax) / np.float32(127.0))
+            qi = q8[hh, 32 * gi:32 * gi + 32].float()
+            assert qi.abs().max() <= 127
+            if amax > 1e-7:
+                assert qi.abs().max() == 127                          # the largest element maps to +-127
+                # within half a step (plus the rounding of 127/amax), checked in fp64
+                err = (qi.double() * qs[hh, gi].double() - blk.double()).abs().max().item()
+                assert err <= qs[hh, gi].item() * 0.5 * (1 + 1e-5)
+    assert torch.all(q8[:, lq:] == 0)                                 # padded rows are zero
+
+
+def test_int8_round_half_even_ties_and_zero_group():
+    # amax = 127 -> recip = 1, so the quantised value is the rounded input itself
+    row = torch.zeros(32, 1, 128)
+    row[0, 0, 0] = 127.0
+    row[1, 0, :8] = torch.tensor([2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5, 126.5])
+    q8, qs = emu.quant_q(row.to(torch.bfloat16))
+    assert qs[0, 0].item() == pytest.approx(1.0)
+    assert q8[0, 1, :8].tolist() == [2, 4, -2, -4, 0, 0, 2, 126]
+    assert torch.all(q8[0, 32:] == 0) and qs[0, 1].item() == np.float32(np.float32(1e-7) / np.float32(127))
+
+
+def test_last_group_counts_padding_as_zero():
+    # Lq = 33: group 1 holds one real row; its scale comes from that row alone
+    q = torch.zeros(33, 1, 128)
+    q[:32] = 100.0
+    q[32, 0, 5] = -3.0
+    q8, qs = emu.quant_q(q.to(torch.bfloat16))
+    assert qs[0, 1].item() == np.float32(np.float32(3.0) / np.float32(127))
+    assert q8[0, 32, 5].item() == -127
+
+
+# ---------------------------------------------------------------- K mean (fixed order) and smoothing
+
+def mean_by_loops(k):
+    """The documented mean order, restated with scalar fp32 loops (tiny inputs only)."""
+    n, h, d = k.shape
+    nb = (n + 63) // 64
+    out = np.zeros((h, d), dtype=np.float32)
+    x = np.zeros((nb * 64, h, d), dtype=np.float32)
+    x[:n] = k.float().numpy()
+    for hh in range(h):
+        for c in range(d):
+            tot = np.float32(0)
+            for b in range(nb):
+                blk = np.float32(0)
+                for rg in range(16):
+                    s = np.float32(0)
+                    for i in range(4):
+                        s = np.float32(s + x[64 * b + rg + 16 * i, hh, c])
+                    blk = np.float32(blk + s)
+                tot = np.float32(tot + blk)
+            out[hh, c] = np.float32(tot / np.float32(n))
+    return torch.from_numpy(out).to(torch.bfloat16).float()
+
+
+def test_chunk_mean_order_and_accuracy():
+    torch.manual_seed(2)
+    k = (torch.randn(150, 2, 4) * 3 + torch.tensor([1e3, -7.0, 0.01, 50.0])).to(torch.bfloat16)
+    km = emu.chunk_mean(k)
+    assert torch.equal(km, mean_by_loops(k))
+    exact = k.double().mean(dim=0)
+    ulp = torch.tensor([2.0 ** (math.floor(math.log2(abs(v))) - 7) for v in exact.flatten().tolist()]).view(2, 4)
+    assert torch.all((km.double() - exact).abs() <= ulp)              # within one bf16 ulp of the true mean
+
+
+def test_smoothing_makes_k8_invariant_to_channel_offsets():
+    # zero-mean noise on a 1/4 grid keeps every fp32 partial sum exact, so the mean is exactly the offset and
+    # K - mean is exactly the noise: the int8 K and its scales cannot depend on the offset
+    rng = np.random.default_rng(3)
+    noise = rng.integers(-16, 17, size=(64, 2, 128)).astype(np.float32) / 4
+    noise = np.concatenate([noise, -noise])                          # 128 tokens, column sums exactly 0
+    outs = []
+    for off in (0.0, 5.5, -24.75):
+        k = torch.from_numpy(noise + np.float32(off)).to(torch.bfloat16)
+        km = emu.chunk_mean(k)
+        assert torch.all(km == off)
+        outs.append(emu.quant_k(k, km))
+    for k8, ks in outs[1:]:
+        assert torch.equal(k8, outs[0][0]) and torch.equal(ks, outs[0][1])
+
+
+# ---------------------------------------------------------------- V planes and layout
+
+def test_v_position_map_is_a_bijection():
+    assert sorted(emu.V_KEY_OF_POS.tolist()) == list(range(64))
+    assert np.array_equal(emu.V_POS_OF_KEY[emu.V_KEY_OF_POS], np.arange(64))
+
+
+def test_v_quant_layout_and_two_term_bound():
+    torch.manual_seed(4)
+    n, h = 130, 2
+    v = (torch.randn(n, h, 128) * torch.rand(1, h, 128) * 4).to(torch.bfloat16)
+    v8, v8lo, vs = emu.quant_v(v)
+    assert v8.shape == (h, 3, 128, 64)
+    amax = v.float().abs().amax(dim=0)
+    assert torch.equal(vs, amax / torch.full_like(amax, 448.0))
+    y = v.float().permute(1, 0, 2) * (torch.full_like(amax, 448.0) / amax)[:, None, :]   # [h, n, d]
+    chunk = {"v8": v8, "v8lo": v8lo, "n": n}
+    one = emu.dequant_v(chunk, terms=1)
+    two = emu.dequant_v(chunk, terms=2)
+    # one e4m3 term: half an e4m3 step (2^-4 relative, 2^-10 absolute in the subnormal range)
+    tol1 = torch.maximum(y.abs() * 2.0 ** -4, torch.full_like(y, 2.0 ** -10))
+    assert torch.all((one - y).abs() <= tol1)
+    # two terms: the residual (at most half a step of hi) carried to e4m3 precision again
+    tol2 = torch.maximum(y.abs() * 2.0 ** -8, torch.full_like(y, 2.0 ** -13))
+    assert torch.all((two - y).abs() <= tol2)
+    assert (two - y).abs().mean() < (one - y).abs().mean() / 8
+    # the channel max lands exactly on 448
+    pos = y.abs().argmax(dim=1)
+    assert torch.all(one.gather(1, pos[:, None, :]).abs() == 448)
+
+
+# ---------------------------------------------------------------- logits
+
+def test_qk_logits_exact_against_int64():
+    rng = np.random.default_rng(5)
+    q8 = rng.integers(-127, 128, size=(2, 64, 128)).astype(np.int8)
+    k8 = rng.integers(-127, 128, size=(2, 96, 128)).astype(np.int8)
+    q8[0, 0] = 127
+    k8[0, 0] = 127                                                   # |S| at its maximum, 127^2 * 128
+    got = emu.qk_logits(torch.from_numpy(q8), torch.from_numpy(k8))
+    want = np.einsum("hqd,hkd->hqk", q8.astype(np.int64), k8.astype(np.int64))
+    assert got.dtype == torch.int32 and np.array_equal(got.numpy(), want)
+    assert want[0, 0, 0] == 127 * 127 * 128
+
+
+# ---------------------------------------------------------------- attention
+
+def test_attention_within_tolerance_of_fp32_softmax():
+    q, k, v, _ = emu.make_inputs(300, 700, h=2, seed=6)
+    out = emu.attention(q, [emu.requant(k, v)])
+    ref = emu.sdpa_fp32(q, k, v)
+    assert (out - ref).abs().max() < 2e-2 and (out - ref).abs().mean() < 2e-3
+    # against torch's own SDPA, so the fp32 reference itself is pinned
+    qt, kt, vt = (x[0].float().transpose(0, 1) for x in (q, k, v))
+    sd = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt).transpose(0, 1)
+    assert torch.allclose(ref, sd, atol=1e-5)
+
+
+def test_attention_invariances():
+    q, k, v, _ = emu.make_inputs(128, 320, h=1, seed=7)
+    base = emu.attention(q, [emu.requant(k, v)])
+    # V scaled by 2: identical e4m3 planes, doubled scale -> exactly doubled output
+    v2 = (v.float() * 2).to(torch.bfloat16)
+    assert torch.equal(emu.attention(q, [emu.requant(k, v2)]), base * 2)
+    # keys shifted by a per-channel constant: with column sums exactly zero on a 1/4 grid the mean is exactly
+    # the shift, K - mean is exactly the unshifted keys, and (one chunk, no bias) the output is identical
+    half = torch.clamp(torch.round(k.float()[:, :160] * 4) / 4, -15, 15)
+    kq = torch.cat([half, -half], dim=1).to(torch.bfloat16)
+    shift = (torch.arange(128) % 25 - 12).float()                     # integers keep kq + shift bf16-exact
+    shifted = (kq.float() + shift).to(torch.bfloat16)
+    assert torch.equal(shifted.float() - shift, kq.float())
+    a = emu.attention(q, [emu.requant(kq, v)])
+    b = emu.attention(q, [emu.requant(shifted, v)])
+    assert torch.equal(a, b)
+
+
+def test_chunked_attention_bias_matches_single_chunk():
+    """Splitting the keys into chunks with their own means (bias q . mean_c) computes the same softmax."""
+    q, k, v, _ = emu.make_inputs(128, 640, h=1, seed=8)
+    one = emu.attention_exact_max(q, [emu.requant(k, v)])
+    parts = [emu.requant(k[:, i:i + 160], v[:, i:i + 160]) for i in range(0, 640, 160)]
+    four = emu.attention_exact_max(q, parts)
+    sd = emu.sdpa_fp32(q, k, v)
+    assert (four - sd).abs().mean() < 1.2 * (one - sd).abs().mean()
+    assert (four - one).abs().max() < 2e-2
+
+
+def test_online_and_exact_max_agree():
+    """The kernel's online max (lazy rescale) and the exact row max round P to e4m3 at different offsets:
+    independent roundings of the same size, so both land equally close to fp32 softmax attention."""
+    q, k, v, _ = emu.make_inputs(256, 1000, h=1, seed=9)
+    ch = [emu.requant(k, v)]
+    sd = emu.sdpa_fp32(q, k, v)
+    e_on = (emu.attention(q, ch) - sd).abs()
+    e_ex = (emu.attention_exact_max(q, ch) - sd).abs()
+    assert 0.8 < e_on.mean() / e_ex.mean() < 1.25
+    assert e_on.max() < 2e-2 and e_ex.max() < 2e-2
+
+
+def test_split_merge_closed_form():
+    torch.manual_seed(10)
+    s = torch.randn(16, 90, dtype=torch.float64) * 3
+    vv = torch.randn(90, 8, dtype=torch.float64)
+    ref = torch.softmax(s, dim=1) @ vv
+    parts = []
+    for a, b in ((0, 31), (31, 64), (64, 90)):
+        m = (s[:, a:b] * emu.LOG2E).amax(dim=1)
+        p = torch.exp2(s[:, a:b] * emu.LOG2E - m[:, None])
+        parts.append((p @ vv[a:b], m, p.sum(dim=1)))
+    assert torch.allclose(emu.merge_partials(parts), ref, atol=1e-12)
+
+
+def test_schedule_covers_every_block_once():
+    for n_tiles, nb, gx in ((576, 378, 64), (144, 24, 64), (3, 2, 64), (1, 1, 32), (100, 7, 16)):
+        sched = emu.attn_schedule(n_tiles, nb, gx)
+        for t in range(n_tiles):
+            blocks = [j for j0, j1 in sched[t] for j in range(j0, j1)]
+            assert blocks == list(range(nb)), (n_tiles, nb, gx, t)
