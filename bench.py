@@ -9,7 +9,8 @@ Reported (one JSON line on stdout):
   value        attention TOPS of the whole call = 4 * H * Lq * Lk * d / step time
   roofline     the attention call alone (attn_fwd_kernel and the small merge of split query tiles, one
                lbw_attn_fwd): algorithmic ops per call / its HIP-event time vs 5.0 POPS dense INT8/FP8 MFMA
-  requant      the K/V re-quant of a saved chunk for 30 layers in one call, algorithmic GB/s vs 8 TB/s
+  requant      the K/V re-quant of a saved chunk for 30 layers in one call: algorithmic bytes (bf16 K, V read
+               once; int8 K and one e4m3 V plane written once; scales) / time, vs 8 TB/s
   cpu_baseline the torch CPU emulation of the same scheme (oracle/emu.py) on a bounded sample of the call
 """
 import argparse
@@ -57,21 +58,23 @@ def attention_ops(lq, lk, h=H, d=D, b=1):
     return 4.0 * b * h * lq * lk * d
 
 
-def requant_bytes(n, h=H, d=D, v_planes=2):
-    """Algorithmic bytes of one chunk's K/V re-quant: bf16 K and V read once; int8 K and the e4m3 V plane(s)
-    written once; one fp32 scale per 64-token K block; fp32 mean and V scale per (head, channel)."""
+def requant_bytes(n, h=H, d=D, v_planes=1):
+    """Bytes of one chunk's K/V re-quant: bf16 K and V read once; int8 K and `v_planes` e4m3 V planes written
+    once; one fp32 scale per 64-token K block; fp32 mean and V scale per (head, channel). With one V plane this
+    is the algorithmic count (55,607,760 B per layer at 6032 tokens x 12 heads); the second (residual) plane
+    this build also writes is overhead on top of it."""
     nb = (n + 63) // 64
     return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + 2 * h * d * 4
 
 
 def traffic_from_profiles():
-    """HBM bytes per attention launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the
-    copy-kernel calibration), committed in profiles/; None when not measured."""
+    """HBM bytes of one attention call (attn_fwd_kernel + merge) measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by a copy of known size), as committed in profiles/; None when not measured."""
     p = os.path.join(ROOT, "profiles", "attn_fwd_cfg3_traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        return json.load(f).get("call_hbm_bytes")
 
 
 def cpu_baseline(heads=3, q_rows=LQ):
@@ -213,6 +216,7 @@ def main():
         rq.write_layers(kl, vl)
     rq_ms = _timed(lambda: rq.write_layers(kl, vl), 10, stream)
     rq_bytes = LAYERS * requant_bytes(CHUNK, H, D)
+    rq_moved = LAYERS * requant_bytes(CHUNK, H, D, v_planes=2)
     rq_gbps = rq_bytes / (rq_ms * 1e-3) / 1e9
     del kl, vl, rq
 
@@ -237,8 +241,9 @@ def main():
                      "traffic": traffic_from_profiles(),
                      "kernel": "lbw_attn_fwd = attn_fwd_kernel + attn_merge_kernel", "kernel_ms": round(attn_ms, 4),
                      "ops_per_launch": ops},
-        "requant": {"layers": LAYERS, "ms": round(rq_ms, 4), "bytes": rq_bytes, "GB/s": round(rq_gbps, 1),
-                    "frac_hbm": round(rq_gbps / HBM_PEAK_GBPS, 4)},
+        "requant": {"layers": LAYERS, "ms": round(rq_ms, 4), "algorithmic_bytes": rq_bytes,
+                    "GB/s": round(rq_gbps, 1), "frac_hbm": round(rq_gbps / HBM_PEAK_GBPS, 4),
+                    "bytes_moved_two_v_planes": rq_moved},
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_heads)

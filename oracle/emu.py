@@ -432,9 +432,9 @@ def attention_ops(lq, lk, h, d=HEAD_DIM, b=1):
     return 4.0 * b * h * lq * lk * d
 
 
-def requant_bytes(n, h, d=HEAD_DIM, v_planes=V_TERMS):
-    """Algorithmic bytes of one chunk's re-quant: read bf16 K and V once, write int8 K and the e4m3 V plane(s)
-    once, plus the per-block K scales and the per-channel mean and V scale."""
+def requant_bytes(n, h, d=HEAD_DIM, v_planes=1):
+    """Bytes of one chunk's re-quant: read bf16 K and V once, write int8 K and `v_planes` e4m3 V planes once,
+    plus the per-block K scales and the per-channel mean and V scale (one plane: the algorithmic count)."""
     nb = pad_to(n, K_BLOCK) // K_BLOCK
     return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + 2 * h * d * 4
 

@@ -122,7 +122,7 @@ def test_bench_inputs_and_counts_match_the_tests():
     for (xk, xv), (yk, yv) in zip(a[3], b[3]):
         assert torch.equal(xk, yk) and torch.equal(xv, yv)
     assert bench.attention_ops(6032, 24128) == emu.attention_ops(6032, 24128, 12) == 4.0 * 12 * 6032 * 24128 * 128
-    assert bench.requant_bytes(6032) == emu.requant_bytes(6032, 12)
+    assert bench.requant_bytes(6032) == emu.requant_bytes(6032, 12) == 55_607_760
 
 
 def test_bench_refuses_more_than_one_gpu():
