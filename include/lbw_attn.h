@@ -68,7 +68,7 @@ int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len);
  * and Sage's per_warp_int8 K part / per_channel_fp8 (lingbot/layers/sage_preq.py:115-124).
  * k/v element (layer l, batch b, token t, head h, channel d) sits at l*s_layer + b*s_batch + t*s_tok
  * + h*s_head + d. `workspace` holds lbw_kv_requant_workspace_bytes() bytes, 16-byte aligned; its
- * contents need not be preserved between calls. Tokens in [len, ceil64(len)) of the slot are written
+ * contents need not be preserved between calls, and calls that share a workspace must not overlap. Tokens in [len, ceil64(len)) of the slot are written
  * as zero; blocks past ceil64(len) are left untouched (the attention never reads them).
  */
 int lbw_kv_requant(const uint16_t* k, const uint16_t* v,

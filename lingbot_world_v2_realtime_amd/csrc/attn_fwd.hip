@@ -20,6 +20,7 @@
 namespace lbw {
 
 constexpr int XCDS = 8;
+constexpr int XCDS_MAX = 8;
 constexpr int TILE_BYTES = KB * D;   // 8 KB: one 64-key K tile or one 64-key fp8 V block
 
 struct AttnArgs {
@@ -30,6 +31,7 @@ struct AttnArgs {
   int seg_slot[LBW_MAX_SEGMENTS];
   int seg_len[LBW_MAX_SEGMENTS];
   int seg_blk0[LBW_MAX_SEGMENTS + 1];   // first tile-relative block of each chunk; [n_seg] = nb
+  int split0[XCDS_MAX + 1];             // split tiles of XCDs before x (prefix), for the merge grid
 };
 
 // Range of tiles of XCD x and its data-parallel / split phases.
@@ -392,22 +394,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restri
 }
 
 // Combine the pieces of each split tile: O = sum 2^(m_i - M) o_i / sum 2^(m_i - M) l_i
-// (experiments/bench_attn/splitkv/README.md:62). One workgroup per tile; thread = (row, 64-channel half).
+// (experiments/bench_attn/splitkv/README.md:62). Grid: (split tile, 16-row slab) -- only split tiles are
+// launched; 256 threads = 16 rows x 16 lanes, each lane 8 consecutive channels, so a row's 512-byte partial is
+// read by 16 consecutive lanes.
+constexpr int MERGE_ROWS = 16;
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ o_part,
                                                          const float* __restrict__ ml_part,
                                                          uint16_t* __restrict__ out, AttnArgs a) {
-  const int tile = blockIdx.x;
+  const int st = blockIdx.x / (QT / MERGE_ROWS), slab = blockIdx.x % (QT / MERGE_ROWS);
   int x = 0;
-  while (x + 1 < XCDS && tile >= (int)((int64_t)(x + 1) * a.n_tiles / XCDS)) ++x;
+  while (x + 1 < XCDS && st >= a.split0[x + 1]) ++x;
   const XcdPlan p = xcd_plan(a, x);
-  if (tile < p.ts) return;
+  const int tile = p.ts + (st - a.split0[x]);
   const int64_t ua = (int64_t)(tile - p.ts) * a.nb, ub = ua + a.nb;
   // workgroups of this XCD whose unit range meets [ua, ub): owner(u) = floor(((u + 1) gx - 1) / units)
   const int i_a = (int)(((ua + 1) * a.gx - 1) / p.units);
   const int i_b = (int)((ub * a.gx - 1) / p.units);
   const int64_t i_a_u0 = (int64_t)i_a * p.units / a.gx, i_a_u1 = (int64_t)(i_a + 1) * p.units / a.gx;
   if (i_a == i_b && i_a_u0 <= ua && i_a_u1 >= ub) return;   // written whole by one workgroup
-  const int t = threadIdx.x, row = t >> 1, half = t & 1;
+  const int t = threadIdx.x, row = slab * MERGE_ROWS + (t >> 4), c0 = (t & 15) * 8;
   const int64_t q = (int64_t)(tile % a.q_tiles) * QT + row;
   if (q >= a.lq) return;
   float mmax = -INFINITY;
@@ -418,9 +423,9 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
     const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (tile == ft ? 0 : 1);
     mmax = fmaxf(mmax, ml_part[(slot * QT + row) * 2]);
   }
-  float acc[64], den = 0.f;
+  float acc[8], den = 0.f;
 #pragma unroll
-  for (int c = 0; c < 64; ++c) acc[c] = 0.f;
+  for (int c = 0; c < 8; ++c) acc[c] = 0.f;
   for (int ii = i_a; ii <= i_b; ++ii) {
     const int64_t w0 = (int64_t)ii * p.units / a.gx, w1 = (int64_t)(ii + 1) * p.units / a.gx;
     if (w0 == w1 || w1 <= ua || w0 >= ub) continue;
@@ -429,23 +434,21 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
     const float2 ml = *(const float2*)(ml_part + (slot * QT + row) * 2);
     const float wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
     den += wgt * ml.y;
-    const float* op = o_part + (slot * QT + row) * D + half * 64;
-#pragma unroll
-    for (int c = 0; c < 64; c += 4) {
-      const float4 v = *(const float4*)(op + c);
-      acc[c] += wgt * v.x; acc[c + 1] += wgt * v.y; acc[c + 2] += wgt * v.z; acc[c + 3] += wgt * v.w;
-    }
+    const float* op = o_part + (slot * QT + row) * D + c0;
+    const float4 v0 = *(const float4*)op, v1 = *(const float4*)(op + 4);
+    acc[0] += wgt * v0.x; acc[1] += wgt * v0.y; acc[2] += wgt * v0.z; acc[3] += wgt * v0.w;
+    acc[4] += wgt * v1.x; acc[5] += wgt * v1.y; acc[6] += wgt * v1.z; acc[7] += wgt * v1.w;
   }
   const float inv = 1.f / den;
   const int bh = tile / a.q_tiles;
   const int64_t b = bh / a.heads, h = bh % a.heads;
-  uint16_t* dst = out + b * a.o_sb + q * a.o_st + h * a.o_sh + half * 64;
+  uint16_t* dst = out + b * a.o_sb + q * a.o_st + h * a.o_sh + c0;
+  uint32_t w[4];
 #pragma unroll
-  for (int c = 0; c < 64; c += 4) {
-    const uint32_t w0 = f32_to_bf16_bits(acc[c] * inv) | ((uint32_t)f32_to_bf16_bits(acc[c + 1] * inv) << 16);
-    const uint32_t w1 = f32_to_bf16_bits(acc[c + 2] * inv) | ((uint32_t)f32_to_bf16_bits(acc[c + 3] * inv) << 16);
-    *(uint2*)(dst + c) = make_uint2(w0, w1);
-  }
+  for (int c = 0; c < 4; ++c)
+    w[c] = f32_to_bf16_bits(acc[2 * c] * inv) | ((uint32_t)f32_to_bf16_bits(acc[2 * c + 1] * inv) << 16);
+  *(uint2*)dst = make_uint2(w[0], w[1]);        // the output contract guarantees 8-byte alignment
+  *(uint2*)(dst + 4) = make_uint2(w[2], w[3]);
 }
 
 // Debug: S = q8 . k8^T in int32 for one slot, through the same LDS tile layout and MFMA as the attention.
@@ -544,6 +547,11 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   a.n_tiles = (int)(a.q_tiles * a.bh);
   if (const int dv = check_device()) return dv;
   a.gx = attn_wgs_per_xcd();
+  a.split0[0] = 0;
+  for (int x = 0; x < XCDS; ++x) {   // tiles past the whole-tile rounds of each XCD are split (xcd_plan)
+    const int t_lo = (int)((int64_t)x * a.n_tiles / XCDS), t_hi = (int)((int64_t)(x + 1) * a.n_tiles / XCDS);
+    a.split0[x + 1] = a.split0[x] + (t_hi - t_lo) % a.gx;
+  }
   float* o_part = (float*)workspace;
   float* ml_part = o_part + (int64_t)XCDS * a.gx * 2 * QT * D;
   hipStream_t st = (hipStream_t)stream;
@@ -553,7 +561,9 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   else
     hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3((unsigned)(XCDS * a.gx)), dim3(256), 0, st, q8, q_scale, bias,
                        k8, k_scale, v8, v8lo, v_scale, out, o_part, ml_part, a);
-  hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)a.n_tiles), dim3(256), 0, st, o_part, ml_part, out, a);
+  if (a.split0[XCDS] > 0)
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a.split0[XCDS] * (QT / MERGE_ROWS))), dim3(256), 0, st,
+                       o_part, ml_part, out, a);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }

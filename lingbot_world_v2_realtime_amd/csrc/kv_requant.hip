@@ -1,14 +1,18 @@
 // K/V re-quant of finished chunks into the quantised ring cache (gfx950).
 //
-// Three launches, all over (64-token block, batch*head, layer):
-//   1. kv_stats:    per block, fp32 column sums of K and column max |V| (read K and V once).
-//   2. kv_finalize: per (layer, bh, channel), sum the block sums left to right, mean -> bf16, V scale.
+// Three launches:
+//   1. kv_stats:    per 64-token block (grid: block, batch*head, layer), fp32 column sums of K and column max |V|
+//                   (K and V read once).
+//   2. kv_finalize: per (batch*head, layer), all of the group's block partials loaded at once, then the
+//                   fixed-order mean -> bf16, the V scale and its reciprocal.
 //   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * (448 / amax) -> e4m3 hi = rn(y) and, when a
-//                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K
-//                   and V a second time; a layer's 37 MB is normally still in the MALL).
-// The column-sum order is fixed (see the oracle's chunk_mean): s = x[rg] + x[rg+16] + x[rg+32] + x[rg+48]
-// per thread, then rg = 0..15 left to right per block, then the blocks left to right, so the mean is the
-// same bits on every run and on the CPU.
+//                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K and
+//                   V a second time).
+// The column-sum order is fixed (see the oracle's chunk_mean): s = x[4q] + x[4q+1] + x[4q+2] + x[4q+3] per
+// thread, q = 0..15 left to right per block, the blocks of each 4-block super-block left to right, then the
+// super-blocks left to right, so the mean is the same bits on every run and on the CPU.
+#include <algorithm>
+
 #include "lbw_common.h"
 
 namespace lbw {
@@ -19,6 +23,10 @@ struct ReqArgs {
   int64_t v_sl, v_sb, v_st, v_sh;
 };
 
+constexpr int REQ_SUPER = 4;   // blocks per super-block of the mean's defined order
+constexpr int FIN_U = 32;      // super-block sums the finaliser holds in LDS at a time
+
+// Thread (cg, q) = (t & 15, t >> 4) sums channels 8 cg .. + 8 over tokens 4 q .. 4 q + 3 of the block.
 __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, ReqArgs a,
                                                        float* __restrict__ part_sum,
@@ -26,7 +34,7 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
   __shared__ float s_sum[16][D];
   __shared__ float s_max[16][D];
   const int blk = blockIdx.x, bh = blockIdx.y, layer = blockIdx.z;
-  const int t = threadIdx.x, cg = t & 15, rg = t >> 4;
+  const int t = threadIdx.x, cg = t & 15, q = t >> 4;
   const int64_t b = bh / a.heads, h = bh % a.heads;
   const uint16_t* kp = k + layer * a.k_sl + b * a.k_sb + h * a.k_sh + cg * 8;
   const uint16_t* vp = v + layer * a.v_sl + b * a.v_sb + h * a.v_sh + cg * 8;
@@ -35,21 +43,17 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
   for (int c = 0; c < 8; ++c) { s[c] = 0.f; m[c] = 0.f; }
   v4i kw[4], vw[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t tok = (int64_t)blk * KB + rg + 16 * i;
-    if (tok < a.len) {
-      kw[i] = *(const v4i*)(kp + tok * a.k_st);
-      vw[i] = *(const v4i*)(vp + tok * a.v_st);
-    } else {
-      kw[i] = v4i{0, 0, 0, 0};
-      vw[i] = v4i{0, 0, 0, 0};
-    }
+  for (int j = 0; j < 4; ++j) {
+    const int64_t tok = (int64_t)blk * KB + 4 * q + j;
+    const bool ok = tok < a.len;
+    kw[j] = ok ? *(const v4i*)(kp + tok * a.k_st) : v4i{0, 0, 0, 0};
+    vw[j] = ok ? *(const v4i*)(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int j = 0; j < 4; ++j) {
     float kf[8], vf[8];
-    unpack8(kw[i], kf);
-    unpack8(vw[i], vf);
+    unpack8(kw[j], kf);
+    unpack8(vw[j], vf);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       s[c] = __fadd_rn(s[c], kf[c]);
@@ -58,8 +62,8 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
   }
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    s_sum[rg][cg * 8 + c] = s[c];
-    s_max[rg][cg * 8 + c] = m[c];
+    s_sum[q][cg * 8 + c] = s[c];
+    s_max[q][cg * 8 + c] = m[c];
   }
   __syncthreads();
   if (t < D) {
@@ -75,24 +79,55 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
   }
 }
 
-__global__ __launch_bounds__(128) void kv_finalize_kernel(ReqArgs a, const float* __restrict__ part_sum,
+// One workgroup per (batch*head, layer). Super-block sums U[u] = B[4u] + .. + B[4u+3] are formed in parallel
+// (thread t: channel t & 127, super-blocks t >> 7, + 2, ..), then summed left to right per channel.
+__global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float* __restrict__ part_sum,
                                                           const float* __restrict__ part_amax,
-                                                          float* __restrict__ v_recip,
-                                                          float* __restrict__ km,
+                                                          float* __restrict__ v_recip, float* __restrict__ km,
                                                           float* __restrict__ v_scale) {
-  const int bh = blockIdx.x, layer = blockIdx.y, c = threadIdx.x;
-  const int64_t base = ((int64_t)layer * a.bh + bh) * a.nb * D + c;
+  __shared__ float buf[FIN_U * D];
+  __shared__ float fin[D];
+  const int bh = blockIdx.x, layer = blockIdx.y;
+  const int t = threadIdx.x, c = t & (D - 1), half = t >> 7;
+  const int64_t grp = (int64_t)layer * a.bh + bh;
+  const float* bsum = part_sum + grp * a.nb * D + c;
+  const float* bmax = part_amax + grp * a.nb * D + c;
+  const int nsup = (int)((a.nb + REQ_SUPER - 1) / REQ_SUPER);
   float tot = 0.f, mx = 0.f;
-  for (int64_t b = 0; b < a.nb; ++b) {
-    tot = __fadd_rn(tot, part_sum[base + b * D]);
-    mx = fmaxf(mx, part_amax[base + b * D]);
+  for (int u0 = 0; u0 < nsup; u0 += FIN_U) {
+    const int nu = min(FIN_U, nsup - u0);
+#pragma unroll 4
+    for (int uu = half; uu < nu; uu += 2) {
+      const int b0 = (u0 + uu) * REQ_SUPER;
+      float bs[REQ_SUPER], bm[REQ_SUPER];
+#pragma unroll
+      for (int i = 0; i < REQ_SUPER; ++i) {
+        const bool ok = b0 + i < a.nb;
+        bs[i] = ok ? bsum[(int64_t)(b0 + i) * D] : 0.f;
+        bm[i] = ok ? bmax[(int64_t)(b0 + i) * D] : 0.f;
+      }
+      float us = 0.f;   // absent blocks add +0, which leaves the sum unchanged
+#pragma unroll
+      for (int i = 0; i < REQ_SUPER; ++i) {
+        us = __fadd_rn(us, bs[i]);
+        mx = fmaxf(mx, bm[i]);
+      }
+      buf[uu * D + c] = us;
+    }
+    __syncthreads();
+    if (t < D)
+      for (int uu = 0; uu < nu; ++uu) tot = __fadd_rn(tot, buf[uu * D + c]);
+    __syncthreads();
   }
-  const float mean = __fdiv_rn(tot, (float)a.len);
-  mx = fmaxf(mx, AMAX_FLOOR);
-  const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + c;
-  km[so] = bf16_round(mean);
-  v_scale[so] = __fdiv_rn(mx, V_MAX);
-  v_recip[((int64_t)layer * a.bh + bh) * D + c] = __fdiv_rn(V_MAX, mx);
+  if (t >= D) fin[c] = mx;
+  __syncthreads();
+  if (t < D) {
+    mx = fmaxf(fmaxf(mx, fin[c]), AMAX_FLOOR);
+    const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + c;
+    km[so] = bf16_round(__fdiv_rn(tot, (float)a.len));
+    v_scale[so] = __fdiv_rn(mx, V_MAX);
+    v_recip[grp * D + c] = __fdiv_rn(V_MAX, mx);
+  }
 }
 
 // Thread t owns channels 8*(t & 15) .. +8 and the 4 consecutive keys 4*(t >> 4) .. +4 of the block, so its
@@ -229,8 +264,8 @@ extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t laye
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
   hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
-  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers), dim3(128), 0, st, a,
-                     part_sum, part_amax, v_recip, km, v_scale);
+  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers), dim3(256), 0, st, a, part_sum,
+                     part_amax, v_recip, km, v_scale);
   hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;

@@ -23,10 +23,12 @@ quantisers and its documentation of the fused kernel:
   (a constant per (query, chunk), so it drops out when there is only one chunk).
 
 Order of the K mean (fixed so it is reproducible bit for bit): token t of a chunk sits in 64-token block
-b = t // 64 at row r = t % 64 = rg + 16 * i (rg in 0..15, i in 0..3). In fp32, starting from +0:
-  s[b, rg] = (((0 + x[rg]) + x[rg + 16]) + x[rg + 32]) + x[rg + 48]
-  B[b]     = s[b, 0] + s[b, 1] + ... + s[b, 15]        (left to right)
-  total    = B[0] + B[1] + ... + B[nb - 1]              (left to right)
+b = t // 64 at row r = t % 64 = 4 q + j (q in 0..15, j in 0..3); blocks form super-blocks of 4 (u = b // 4).
+In fp32, every sum starting from +0 and running left to right:
+  s[b, q]  = x[4q] + x[4q + 1] + x[4q + 2] + x[4q + 3]
+  B[b]     = s[b, 0] + s[b, 1] + ... + s[b, 15]
+  U[u]     = B[4u] + B[4u + 1] + B[4u + 2] + B[4u + 3]     (the blocks that exist)
+  total    = U[0] + U[1] + ... + U[nsup - 1]
   mean     = total / n (fp32, correctly rounded), km = bf16(mean) round to nearest even.
 Padding tokens past n add +0.
 
@@ -41,6 +43,7 @@ import torch
 Q_GROUP = 32            # query rows per Q scale
 Q_TILE = 128            # Lq is padded to whole tiles of this many rows (the attention tile)
 K_BLOCK = 64            # keys per K scale and per V block
+SUPER_BLOCK = 4         # K blocks per partial sum of the mean
 HEAD_DIM = 128
 V_MAX = 448.0           # e4m3 max; the V scale maps amax to it
 AMAX_FLOOR = 1e-7
@@ -121,16 +124,19 @@ def chunk_mean(k):
     nb = pad_to(n, K_BLOCK) // K_BLOCK
     x = torch.zeros(nb * K_BLOCK, h, d, dtype=torch.float32)
     x[:n] = k.float()
-    x = x.view(nb, 4, 16, h, d)                  # [b, i, rg, h, d]: token = 64 b + rg + 16 i
+    x = x.view(nb, 16, 4, h, d)                  # [b, q, j, h, d]: token = 64 b + 4 q + j
     s = torch.zeros(nb, 16, h, d, dtype=torch.float32)
-    for i in range(4):
-        s = s + x[:, i]
+    for j in range(4):
+        s = s + x[:, :, j]
     blk = torch.zeros(nb, h, d, dtype=torch.float32)
-    for rg in range(16):
-        blk = blk + s[:, rg]
+    for q in range(16):
+        blk = blk + s[:, q]
     tot = torch.zeros(h, d, dtype=torch.float32)
-    for b in range(nb):
-        tot = tot + blk[b]
+    for u in range(0, nb, SUPER_BLOCK):
+        sup = torch.zeros(h, d, dtype=torch.float32)
+        for b in range(u, min(nb, u + SUPER_BLOCK)):
+            sup = sup + blk[b]
+        tot = tot + sup
     mean = tot / torch.tensor(float(n), dtype=torch.float32)
     return bf16_round(mean)
 

@@ -76,6 +76,26 @@ def test_requant_layers_and_strides():
         _check_chunk(ring, l + 1, 2, ref, n)
 
 
+def test_requant_30_layers():
+    """The bench shape: 30 layers x 12 heads x 6032 tokens in one call (360 (layer, head) groups, launched as
+    stats / quant pairs over groups of layers), sampled layers bit-exact, also on a second call into the same
+    workspace."""
+    layers, h, n = 30, 12, 6032
+    g = torch.Generator(device=DEV).manual_seed(30)
+    k = (torch.randn(layers, 1, n, h, 128, device=DEV, generator=g) * 2 +
+         torch.randn(layers, 1, 1, h, 128, device=DEV, generator=g) * 3).to(torch.bfloat16)
+    v = (torch.randn(layers, 1, n, h, 128, device=DEV, generator=g) * 1.5).to(torch.bfloat16)
+    ring = _ring(layers, h, n, slots=4)
+    ws = _k().requant_workspace(layers, h, n, DEV)
+    for call in range(2):
+        _k().kv_requant(k, v, ring, slot=call + 1, workspace=ws)
+        torch.cuda.synchronize()
+    for l in (0, 13, 29):
+        ref = emu.requant(k[l].cpu(), v[l].cpu())
+        for slot in (1, 2):
+            _check_chunk(ring, l, slot, ref, n)
+
+
 @pytest.mark.parametrize("lq", [1, 31, 32, 100, 1508])
 def test_quant_q_bit_exact(lq):
     torch.manual_seed(lq)

@@ -107,21 +107,24 @@ def mean_by_loops(k):
     for hh in range(h):
         for c in range(d):
             tot = np.float32(0)
-            for b in range(nb):
-                blk = np.float32(0)
-                for rg in range(16):
-                    s = np.float32(0)
-                    for i in range(4):
-                        s = np.float32(s + x[64 * b + rg + 16 * i, hh, c])
-                    blk = np.float32(blk + s)
-                tot = np.float32(tot + blk)
+            for u in range(0, nb, 4):
+                sup = np.float32(0)
+                for b in range(u, min(nb, u + 4)):
+                    blk = np.float32(0)
+                    for q in range(16):
+                        s = np.float32(0)
+                        for j in range(4):
+                            s = np.float32(s + x[64 * b + 4 * q + j, hh, c])
+                        blk = np.float32(blk + s)
+                    sup = np.float32(sup + blk)
+                tot = np.float32(tot + sup)
             out[hh, c] = np.float32(tot / np.float32(n))
     return torch.from_numpy(out).to(torch.bfloat16).float()
 
 
 def test_chunk_mean_order_and_accuracy():
     torch.manual_seed(2)
-    k = (torch.randn(150, 2, 4) * 3 + torch.tensor([1e3, -7.0, 0.01, 50.0])).to(torch.bfloat16)
+    k = (torch.randn(700, 2, 4) * 3 + torch.tensor([1e3, -7.0, 0.01, 50.0])).to(torch.bfloat16)
     km = emu.chunk_mean(k)
     assert torch.equal(km, mean_by_loops(k))
     exact = k.double().mean(dim=0)
