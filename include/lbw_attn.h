@@ -27,7 +27,7 @@
  * With the second plane, V = (hi + lo / 16) * v_scale to about 7 significant bits instead of 4.
  * Position p of a 64-key V block holds key 32*((p&31)>>4) + 8*((p>>2)&3) + 4*(p>>5) + (p&3).
  *
- * Quantised Q (per call): q8 int8 [BH][Lp][128], q_scale fp32 [BH][Lp/32], Lp = Lq rounded up to 128;
+ * Quantised Q (per call): q8 int8 [BH][Lp][128], q_scale fp32 [BH][Lp/32], Lp = Lq rounded up to 256;
  * bias fp32 [n_seg][BH][Lp] holds q . km of each attended chunk (only read when n_seg > 1).
  */
 #ifndef LBW_ATTN_H

@@ -1,13 +1,14 @@
 // Quantized attention forward for gfx950: int8 QK^T on v_mfma_i32_32x32x32_i8, online softmax in the exp2
 // domain, e4m3 P times e4m3 V on v_mfma_f32_32x32x64_f8f6f4, fp32 accumulation.
 //
-// Tile: 4 waves x 32 queries = 128 queries of one batch*head. Each wave computes S^T = K Q^T (keys on the MFMA
+// Tile: 8 waves x 32 queries = 256 queries of one batch*head. Each wave computes S^T = K Q^T (keys on the MFMA
 // M axis, queries on N), so a lane holds one query and 16 keys of each 32x32 S tile: the row max and row sum
 // are in-lane plus one exchange with lane ^ 32 (v_permlane32_swap), and the S tile's register layout is directly
 // the B operand (P^T) of the PV product O^T = V^T P^T because the fp8 V block stores its keys in that order.
-// K / V blocks of 64 keys (8 KB each) stream through LDS, double buffered: the next block's global loads are in
-// flight while the current one is computed. The int32 accumulator starts at the bits of 1.5 * 2^23, so its
-// result reads directly as the float 12582912 + S (|S| <= 2^21): the int -> float conversion is free.
+// The int32 accumulator starts at the bits of 1.5 * 2^23, so its result reads directly as the float
+// 12582912 + S (|S| <= 2^21): the int -> float conversion is free. The two 4-wave halves of the workgroup run
+// phase-shifted (one half's MFMAs under the other half's softmax); K / V blocks of 64 keys reach LDS by direct
+// global -> LDS loads several blocks ahead (see attend_range).
 //
 // Scheduling: a persistent grid of `gx` workgroups per XCD (workgroup g runs on XCD g % 8). The query tiles
 // (head-major, so one head's tiles are contiguous) are split into 8 contiguous ranges, one per XCD, so each
@@ -119,16 +120,59 @@ struct Piece {      // online-softmax state of one wave after a range of key blo
   int c_last;       // chunk of the last block processed
 };
 
-// Key blocks [j0, j1) of one tile for this wave's 32 queries. TWO: V has a second (residual) e4m3 plane.
+// ---- 8-wave ping-pong attention --------------------------------------------------------------------------
+// A workgroup is 8 waves x 32 queries = a 256-query tile. Waves 0-3 (group A) and 4-7 (group B) share the SIMDs
+// (one wave of each per SIMD) and run the same per-block program with a phase offset of one barrier: while one
+// group issues its MFMAs (S = K Q^T of block j, then P V of block j - 1) the other computes the softmax of its
+// block, so the matrix cores and the vector ALUs work at the same time. Group A also streams the K / V blocks
+// into LDS with direct global -> LDS loads, LEAD blocks ahead, through NSTAGE stages. Stage layout (24 KB):
+// K tile 64 rows x 128 B, V tile 128 channels x 64 B, V residual tile; 16-byte chunks XOR-swizzled by row
+// (K: chunk ^ ((row >> 1) & 7), V: chunk ^ ((row >> 2) & 3)) so that the fragment reads of the MFMA operands hit
+// 16 distinct bank groups per 16 lanes, and every 1 KB of a tile is one contiguous DMA of 64 lanes x 16 B.
+constexpr int AT_WAVES = 8;
+constexpr int AT_THREADS = 64 * AT_WAVES;
+constexpr int NSTAGE = 5;
+constexpr int LEAD = 3;                        // NSTAGE - LEAD >= 2: a stage is free one phase before its reload
+constexpr int ST_K = 0, ST_V = 8192, ST_VLO = 16384, ST_BYTES = 24576;
+static_assert(QT == 32 * AT_WAVES, "query tile");
+
+// Workgroup barrier that also stops the compiler from moving memory accesses across it. No wait is implied:
+// the global -> LDS loads a phase depends on are waited for explicitly by the waves that issued them.
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// s_waitcnt on vmcnt only (lgkmcnt and expcnt at their maxima), for n < 16.
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+}
+
+__device__ __forceinline__ void dma16(const void* src, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
 template <bool TWO>
 __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __restrict__ q8,
                                              const float* __restrict__ q_scale, const float* __restrict__ bias,
                                              const int8_t* __restrict__ k8, const float* __restrict__ k_scale,
                                              const uint8_t* __restrict__ v8, const uint8_t* __restrict__ v8lo,
-                                             const float* __restrict__ v_scale,
-                                             uint8_t (*smem)[STAGE_BYTES], int bh, int64_t q0, int j0, int j1,
-                                             Piece& st) {
+                                             const float* __restrict__ v_scale, uint8_t* lds, int bh, int64_t q0,
+                                             int j0, int j1, Piece& st) {
+  constexpr int NPB = TWO ? 6 : 4;   // DMA instructions per block of each loading wave
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform, so the loader's control stays scalar
+  const bool loader = w < 4;
+  const int n = j1 - j0;
   v4i qf[4];
   {
     const int8_t* qrow = q8 + ((int64_t)bh * a.lp + q0 + lq) * D + 64 * g;
@@ -144,92 +188,161 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   v16i magic;
 #pragma unroll
   for (int i = 0; i < 16; ++i) magic[i] = S_MAGIC;
-
-  // chunk and chunk-relative block of j0
-  int c = 0;
-  while (j0 >= a.seg_blk0[c + 1]) ++c;
-  int blk = j0 - a.seg_blk0[c];
   const bool multi = a.n_seg > 1;
 
-  // loader: chunk lc, block lb, uniform base pointers of the block to load next
-  int lc = c, lb = blk;
+  // fragment read offsets in a stage (K: chunk 4g + kk of row 32 mt + lq; V: chunks 2g, 2g + 1 of row 32 mt + lq)
+  int kro[4], vro[2];
+  {
+    const int s1 = (lq >> 1) & 7, s2 = (lq >> 2) & 3;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kro[kk] = lq * 128 + (((4 * g + kk) ^ s1) << 4);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) vro[h] = ST_V + lq * 64 + (((2 * g + h) ^ s2) << 4);
+  }
+
+  // loader (group A): wave wl = w moves 1 KB pieces 2 wl, 2 wl + 1 of each 8 KB tile
+  const int i0 = 2 * (w & 3);
+  int koff[2], voff[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int kr = 8 * (i0 + u) + (lane >> 3), vr = 16 * (i0 + u) + (lane >> 2);
+    koff[u] = kr * 128 + (((lane & 7) ^ ((kr >> 1) & 7)) << 4);
+    voff[u] = vr * 64 + (((lane & 3) ^ ((vr >> 2) & 3)) << 4);
+  }
+  // chunk lengths are only read when a cursor enters a chunk: an indexed read of the arguments is a memory load,
+  // and waiting for it would also wait for every global -> LDS load in flight
+  int lc = 0;
+  while (j0 >= a.seg_blk0[lc + 1]) ++lc;
+  int lrem = a.seg_blk0[lc + 1] - j0;   // blocks the loader has left in chunk lc
+  const int lb = j0 - a.seg_blk0[lc];
   const int8_t* kbase;
   const uint8_t* vbase;
   const uint8_t* vlbase;
-  const float* ksbase;
   auto seek = [&](int cc, int bb) {
     const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
     kbase = k8 + (sbh * a.cap + (int64_t)bb * KB) * D;
     vbase = v8 + (sbh * a.nbc + bb) * TILE_BYTES;
     if (TWO) vlbase = v8lo + (sbh * a.nbc + bb) * TILE_BYTES;
-    ksbase = k_scale + sbh * a.nbc + bb;
   };
   seek(lc, lb);
-  v4i pk0, pk1, pv0, pv1, pl0, pl1;
-  float ks_next = 0.f;
-  auto gload = [&]() {
-    pk0 = *(const v4i*)(kbase + t * 16);
-    pk1 = *(const v4i*)(kbase + 4096 + t * 16);
-    pv0 = *(const v4i*)(vbase + t * 16);
-    pv1 = *(const v4i*)(vbase + 4096 + t * 16);
-    if (TWO) {
-      pl0 = *(const v4i*)(vlbase + t * 16);
-      pl1 = *(const v4i*)(vlbase + 4096 + t * 16);
+  auto issue = [&](int stage) {
+    uint8_t* sb = lds + stage * ST_BYTES;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      dma16(kbase + koff[u], sb + ST_K + (i0 + u) * 1024);
+      dma16(vbase + voff[u], sb + ST_V + (i0 + u) * 1024);
+      if (TWO) dma16(vlbase + voff[u], sb + ST_VLO + (i0 + u) * 1024);
     }
-    ks_next = *ksbase;
   };
   auto advance = [&]() {
-    if (++lb * KB >= a.seg_len[lc]) {
+    if (--lrem == 0) {
       ++lc;
-      lb = 0;
-      if (lc < a.n_seg) seek(lc, 0);
+      if (lc < a.n_seg) {
+        seek(lc, 0);
+        lrem = a.seg_blk0[lc + 1] - a.seg_blk0[lc];
+      }
     } else {
       kbase += TILE_BYTES;
       vbase += TILE_BYTES;
       if (TWO) vlbase += TILE_BYTES;
-      ksbase += 1;
-    }
-  };
-  // per-lane LDS offsets of this thread's stores (thread t: K chunk t and t + 256, V chunk t and t + 256)
-  const int ks_off = k_lds_off(t >> 3, t & 7), vs_off = v_lds_off(t >> 2, t & 3);
-  auto lstore = [&](uint8_t* s) {
-    *(v4i*)(s + ks_off) = pk0;
-    *(v4i*)(s + ks_off + 32 * K_ROW) = pk1;
-    *(v4i*)(s + vs_off) = pv0;
-    *(v4i*)(s + vs_off + 64 * V_ROW) = pv1;
-    if (TWO) {
-      *(v4i*)(s + vs_off + VLO_LDS_OFF) = pl0;
-      *(v4i*)(s + vs_off + VLO_LDS_OFF + 64 * V_ROW) = pl1;
     }
   };
 
+  // compute cursor: chunk c and chunk-relative block blk of the block in the softmax
+  int c = 0;
+  while (j0 >= a.seg_blk0[c + 1]) ++c;
+  int blk = j0 - a.seg_blk0[c];
+  int crem = a.seg_blk0[c + 1] - j0;                   // blocks left in chunk c, this one included
+  int last_valid = a.seg_len[c] - (a.seg_blk0[c + 1] - a.seg_blk0[c] - 1) * KB;   // keys in its last block
+  const float* ksp = k_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * a.nbc + blk;
   float beta = multi ? bias[((int64_t)c * a.bh + bh) * a.lp + q0 + lq] * a.sl2 : 0.f;
-  gload();
-  advance();
-  float ks = ks_next;
-  lstore(smem[0]);
-  __syncthreads();
-  int buf = 0;
+  int c_prev = c;
 
-  for (int j = j0; j < j1; ++j) {
-    const bool more = j + 1 < j1;
-    const int cn = lc, bn = lb;   // the block loaded now is the next one computed
-    if (more) {
-      gload();
+  const int npre = n < LEAD ? n : LEAD;
+  if (loader) {
+    for (int i = 0; i < npre; ++i) {
+      issue(i);
       advance();
     }
+    wait_vm(NPB * (npre - 1));   // the first block has landed
+  }
+  int ldstage = npre % NSTAGE;
+  phase_barrier();
+  if (!loader) phase_barrier();   // group B runs one phase behind
 
-    const uint8_t* sk = smem[buf];
+  v8i pb = {0, 0, 0, 0, 0, 0, 0, 0};
+  int stage = 0, pstage = 0;
+  for (int it = 0;; ++it) {
+    // ---- MFMA phase: S of block it, P V of block it - 1 ----
+    __builtin_amdgcn_s_setprio(1);
     v16i acc[2];
-    qk_tile(sk, qf, lq, g, acc, magic);
+    if (it < n) {
+      const uint8_t* sk = lds + stage * ST_BYTES;
+      acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[0]), qf[0], magic, 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[0] + 4096), qf[0], magic, 0, 0, 0);
+#pragma unroll
+      for (int kk = 1; kk < 4; ++kk) {
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[kk]), qf[kk], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[kk] + 4096), qf[kk], acc[1], 0, 0, 0);
+      }
+    }
+    if (it > 0) {
+      const uint8_t* sv = lds + pstage * ST_BYTES;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        const v4i lo = *(const v4i*)(sv + vro[0] + mt * 2048);
+        const v4i hi = *(const v4i*)(sv + vro[1] + mt * 2048);
+        const v8i vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[mt], 0, 0, 0, 0, 0, 0);
+      }
+      if (TWO) {   // residual plane, accumulated with block scale 2^-4
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          const v4i lo = *(const v4i*)(sv + vro[0] + (ST_VLO - ST_V) + mt * 2048);
+          const v4i hi = *(const v4i*)(sv + vro[1] + (ST_VLO - ST_V) + mt * 2048);
+          const v8i vl = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vl, pb, st.o[mt], 0, 0, 0, E8M0_LO, 0, E8M0_ONE);
+        }
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+    if (it == n) break;
+    phase_barrier();
 
+    // ---- softmax phase for block it (chunk c, block blk); group A streams block it + LEAD ----
+    if (loader && it + LEAD < n) {
+      issue(ldstage);
+      advance();
+      ldstage = ldstage + 1 == NSTAGE ? 0 : ldstage + 1;
+    }
+    if (c != c_prev) {
+      // a new chunk: O (blocks before this one) to its V scale, and its logit bias
+      const float* vs_old = v_scale + ((int64_t)a.seg_slot[c_prev] * a.bh + bh) * D;
+      const float* vs_new = v_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * D;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int ch = 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
+          st.o[mt][i] *= vs_old[ch] / vs_new[ch];
+        }
+      beta = bias[((int64_t)c * a.bh + bh) * a.lp + q0 + lq] * a.sl2;
+      c_prev = c;
+    }
+    float ks;
+    {   // the block's K scale through a provably uniform address: a scalar load
+      const uint64_t ka = (uint64_t)ksp;
+      const uint64_t ku = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(ka >> 32)) << 32) |
+                          (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ka);
+      ks = *(const float*)ku;
+    }
     const float cb = qs_sl2 * ks;
     int si[32];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) si[16 * mt + i] = acc[mt][i];
-    const int valid = a.seg_len[c] - blk * KB;   // keys of this block that exist (>= 1)
+    const int valid = crem == 1 ? last_valid : KB;   // keys of this block that exist (>= 1)
     if (valid < KB) {
       const int vt = valid - 4 * g;   // key 32 mt + 8 (i >> 2) + 4 g + (i & 3) is past the end iff its
 #pragma unroll                        // lane-independent part reaches vt
@@ -256,52 +369,36 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(si[i]), cb, kc));
     l_run += sum32(p);
     // P^T B operand: byte 16 mt' + 4 i + j of this lane = p[16 mt' + 4 i + j] (keys 32 mt' + 8 i + 4 g + j).
-    v8i pb;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       int wd = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * r], p[4 * r + 1], 0, false);
       wd = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * r + 2], p[4 * r + 3], wd, true);
       pb[r] = wd;
     }
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int row = 32 * mt + lq;
-      const v4i lo = *(const v4i*)(sk + v_lds_off(row, 2 * g));
-      const v4i hi = *(const v4i*)(sk + v_lds_off(row, 2 * g + 1));
-      const v8i vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[mt], 0, 0, 0, 0, 0, 0);
-      if (TWO) {   // residual plane, accumulated with block scale 2^-4
-        const v4i lo2 = *(const v4i*)(sk + v_lds_off(row, 2 * g) + VLO_LDS_OFF);
-        const v4i hi2 = *(const v4i*)(sk + v_lds_off(row, 2 * g + 1) + VLO_LDS_OFF);
-        const v8i vl = {lo2[0], lo2[1], lo2[2], lo2[3], hi2[0], hi2[1], hi2[2], hi2[3]};
-        st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vl, pb, st.o[mt], 0, 0, 0, E8M0_LO, 0, E8M0_ONE);
-      }
+    // next block of the compute cursor
+    if (--crem == 0 && c + 1 < a.n_seg) {
+      ++c;
+      blk = 0;
+      crem = a.seg_blk0[c + 1] - a.seg_blk0[c];
+      last_valid = a.seg_len[c] - (crem - 1) * KB;
+      ksp = k_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * a.nbc;
+    } else {
+      ++blk;
+      ++ksp;
     }
-
-    if (more) lstore(smem[buf ^ 1]);
-    __syncthreads();
-    if (!more) break;
-    if (cn != c) {
-      // next chunk: its own V scale (rescale the accumulator per channel) and its own logit bias
-      const float* vs_old = v_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * D;
-      const float* vs_new = v_scale + ((int64_t)a.seg_slot[cn] * a.bh + bh) * D;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int ch = 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
-          st.o[mt][i] *= vs_old[ch] / vs_new[ch];
-        }
-      beta = bias[((int64_t)cn * a.bh + bh) * a.lp + q0 + lq] * a.sl2;
+    if (loader) {   // block it + 1 has landed (blocks up to it + LEAD may still be in flight)
+      const int ahead = (it + LEAD < n ? it + LEAD : n - 1) - (it + 1);
+      wait_vm(ahead > 0 ? NPB * ahead : 0);
     }
-    c = cn;
-    blk = bn;
-    ks = ks_next;
-    buf ^= 1;
+    phase_barrier();
+    pstage = stage;
+    stage = stage + 1 == NSTAGE ? 0 : stage + 1;
   }
+  if (loader) phase_barrier();   // matches group B's extra barrier at the start
+  phase_barrier();               // every wave is done with the stages before they are refilled
   st.m = m_ref;
   st.l = halves_sum(l_run);
-  st.c_last = c;
+  st.c_last = c_prev;
 }
 
 // Whole tile: O = o * v_scale / l as bf16; lane (query lq) writes channels 32 mt + 8 i + 4 g + (0..3).
@@ -351,17 +448,17 @@ __device__ __forceinline__ void store_part(const AttnArgs& a, const Piece& st, c
 }
 
 template <bool TWO>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restrict__ q8,
-                                                          const float* __restrict__ q_scale,
-                                                          const float* __restrict__ bias,
-                                                          const int8_t* __restrict__ k8,
-                                                          const float* __restrict__ k_scale,
-                                                          const uint8_t* __restrict__ v8,
-                                                          const uint8_t* __restrict__ v8lo,
-                                                          const float* __restrict__ v_scale,
-                                                          uint16_t* __restrict__ out, float* __restrict__ o_part,
-                                                          float* __restrict__ ml_part, AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2][STAGE_BYTES];
+__global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* __restrict__ q8,
+                                                                 const float* __restrict__ q_scale,
+                                                                 const float* __restrict__ bias,
+                                                                 const int8_t* __restrict__ k8,
+                                                                 const float* __restrict__ k_scale,
+                                                                 const uint8_t* __restrict__ v8,
+                                                                 const uint8_t* __restrict__ v8lo,
+                                                                 const float* __restrict__ v_scale,
+                                                                 uint16_t* __restrict__ out, float* __restrict__ o_part,
+                                                                 float* __restrict__ ml_part, AttnArgs a) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * ST_BYTES];
   const int gid = blockIdx.x, x = gid % XCDS, i = gid / XCDS;
   const int w = threadIdx.x >> 6;
   const XcdPlan p = xcd_plan(a, x);
@@ -370,7 +467,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restri
   for (int tile = p.t_lo + i; tile < p.ts; tile += a.gx) {
     const int bh = tile / a.q_tiles;
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
-    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, smem, bh, q0, 0, a.nb, st);
+    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, 0, a.nb, st);
     store_out(a, st, v_scale, out, bh, q0);
   }
   // this workgroup's piece of the split tiles
@@ -383,7 +480,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const int8_t* __restri
     const int j1 = (int)((u1 - u + j0 < a.nb) ? (u1 - u + j0) : a.nb);
     const int bh = tile / a.q_tiles;
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
-    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, smem, bh, q0, j0, j1, st);
+    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, j0, j1, st);
     if (j0 == 0 && j1 == a.nb) {
       store_out(a, st, v_scale, out, bh, q0);
     } else {
@@ -451,7 +548,8 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   *(uint2*)(dst + 4) = make_uint2(w[2], w[3]);
 }
 
-// Debug: S = q8 . k8^T in int32 for one slot, through the same LDS tile layout and MFMA as the attention.
+// Debug: S = q8 . k8^T in int32 for one slot, on the same int8 MFMA as the attention (128 queries per workgroup).
+constexpr int LOGIT_ROWS = 128;
 __global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict__ q8,
                                                         const int8_t* __restrict__ k8, int64_t lp,
                                                         int64_t cap, int64_t bh_count, int64_t slot,
@@ -459,7 +557,7 @@ __global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict
   __shared__ __attribute__((aligned(16))) uint8_t smem[K_LDS];
   const int tile = blockIdx.x, blk = blockIdx.y, bh = blockIdx.z;
   const int t = threadIdx.x, w = t >> 6, lane = t & 63, lq = lane & 31, g = lane >> 5;
-  const int64_t q0 = (int64_t)tile * QT + w * 32;
+  const int64_t q0 = (int64_t)tile * LOGIT_ROWS + w * 32;
   v4i qf[4];
   const int8_t* qrow = q8 + ((int64_t)bh * lp + q0 + lq) * D + 64 * g;
 #pragma unroll
@@ -480,15 +578,15 @@ __global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict
     for (int i = 0; i < 16; ++i) op[32 * mt + 8 * (i >> 2) + 4 * g + (i & 3)] = acc[mt][i];
 }
 
-// Persistent workgroups per XCD: two per CU (the kernel fits two 4-wave workgroups per CU).
+// Persistent workgroups per XCD: one per CU (a workgroup is 8 waves, two per SIMD, and uses 120 KB of LDS).
 static int attn_wgs_per_xcd() {
   static int cached[64] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
   if (cached[dev] == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = (cus * 2 + XCDS - 1) / XCDS;
+    cached[dev] = (cus + XCDS - 1) / XCDS;
   }
   return cached[dev];
 }
@@ -556,10 +654,10 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   float* ml_part = o_part + (int64_t)XCDS * a.gx * 2 * QT * D;
   hipStream_t st = (hipStream_t)stream;
   if (v8lo)
-    hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3((unsigned)(XCDS * a.gx)), dim3(256), 0, st, q8, q_scale, bias,
+    hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3((unsigned)(XCDS * a.gx)), dim3(AT_THREADS), 0, st, q8, q_scale, bias,
                        k8, k_scale, v8, v8lo, v_scale, out, o_part, ml_part, a);
   else
-    hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3((unsigned)(XCDS * a.gx)), dim3(256), 0, st, q8, q_scale, bias,
+    hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3((unsigned)(XCDS * a.gx)), dim3(AT_THREADS), 0, st, q8, q_scale, bias,
                        k8, k_scale, v8, v8lo, v_scale, out, o_part, ml_part, a);
   if (a.split0[XCDS] > 0)
     hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a.split0[XCDS] * (QT / MERGE_ROWS))), dim3(256), 0, st,
@@ -575,7 +673,7 @@ extern "C" int lbw_qk_logits_i32(const int8_t* q8, int64_t bh, int64_t lq, const
   if (((uintptr_t)q8 | (uintptr_t)k8) & 15) return LBW_E_ALIGN;
   if (const int dv = check_device()) return dv;
   const int64_t lp = (lq + QT - 1) / QT * QT;
-  hipLaunchKernelGGL(qk_logits_kernel, dim3((unsigned)(lp / QT), (unsigned)(cap / KB), (unsigned)bh), dim3(256),
+  hipLaunchKernelGGL(qk_logits_kernel, dim3((unsigned)(lp / LOGIT_ROWS), (unsigned)(cap / KB), (unsigned)bh), dim3(256),
                      0, (hipStream_t)stream, q8, k8, lp, cap, bh, slot, out);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;

@@ -17,7 +17,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int D = LBW_HEAD_DIM;   // head dim
 constexpr int KB = 64;            // keys per K scale block / V block
 constexpr int QG = 32;            // query rows per Q scale
-constexpr int QT = 128;           // Lq is padded to whole tiles of this many rows (the attention tile)
+constexpr int QT = 256;           // Lq is padded to whole tiles of this many rows (the attention tile)
 constexpr float V_MAX = 448.f;
 constexpr float V_LO_SCALE = 16.f;           // second e4m3 V plane: the residual of the first, times 16
 constexpr float AMAX_FLOOR = 1e-7f;

@@ -8,7 +8,7 @@ from . import _lib
 
 HEAD_DIM = 128
 K_BLOCK = 64
-Q_TILE = 128
+Q_TILE = 256
 Q_GROUP = 32
 MAX_SEGMENTS = 8
 ctypes_i32 = ctypes.c_int32

@@ -41,7 +41,7 @@ import numpy as np
 import torch
 
 Q_GROUP = 32            # query rows per Q scale
-Q_TILE = 128            # Lq is padded to whole tiles of this many rows (the attention tile)
+Q_TILE = 256            # Lq is padded to whole tiles of this many rows (the attention tile)
 K_BLOCK = 64            # keys per K scale and per V block
 SUPER_BLOCK = 4         # K blocks per partial sum of the mean
 HEAD_DIM = 128

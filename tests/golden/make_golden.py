@@ -4,10 +4,10 @@ for them. Run from the repository root: `python tests/golden/make_golden.py`.
 Cases (bf16 inputs stored as their 16-bit patterns, int16):
   requant : K, V [1, 100, 2, 128] (K with a per-channel offset)   -> k8, k_scale, km, v8, v8lo, v_scale
   quant_q : Q [1, 70, 2, 128]                                     -> q8, q_scale
-  logits  : q8 x k8 of the two cases above                        -> int32 [2, 128, 100]
+  logits  : q8 x k8 of the two cases above                        -> int32 [2, 256, 100]
   attn1   : Q [1, 70, 2, 128] over the requant chunk              -> fp32 out [70, 2, 128]
   ring    : Q [1, 70, 2, 128] over chunks of 90, 64 and 100 keys  -> fp32 out [70, 2, 128]
-The attention outputs follow the kernel's schedule for 64 persistent workgroups per XCD (256 CUs)."""
+The attention outputs follow the kernel's schedule for 32 persistent workgroups per XCD (256 CUs)."""
 import os
 import sys
 
@@ -20,7 +20,7 @@ sys.path.insert(0, ROOT)
 from oracle import emu  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden.npz")
-GX = 64
+GX = 32
 
 
 def bits(x):
