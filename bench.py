@@ -11,6 +11,8 @@ Reported (one JSON line on stdout):
                lbw_attn_fwd): algorithmic ops per call / its HIP-event time vs 5.0 POPS dense INT8/FP8 MFMA
   requant      the K/V re-quant of a saved chunk for 30 layers in one call: algorithmic bytes (bf16 K, V read
                once; int8 K and one e4m3 V plane written once; scales) / time, vs 8 TB/s
+  chunk_sweep  the whole chunk captured in one HIP graph: 30 layers x 5 passes of the step above, then the
+               30-layer re-quant that saves the chunk; seconds per chunk
   cpu_baseline the torch CPU emulation of the same scheme (oracle/emu.py) on a bounded sample of the call
 """
 import argparse
@@ -149,6 +151,52 @@ def profile_only(args, dev):
     print(json.dumps({"only": args.only, "launches": args.steps, "ms": round(ms, 4), "bytes": nbytes}), flush=True)
 
 
+def chunk_sweep(dev, layers=LAYERS, passes=5, replays=3):
+    """The whole chunk as the causal DiT runs it: `passes` forwards (4 denoising steps and the clean pass) of
+    `layers` layers, each layer call re-quantising the current chunk's K/V into its ring slot and attending over
+    the current chunk plus 3 cached chunks (Q [1,6032,12,128], 24128 keys), then the 30-layer re-quant that
+    saves the chunk -- captured once in a HIP graph and replayed. Returns seconds per chunk and attention TOPS."""
+    import torch
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    q, k, v, mem = synthetic_inputs(LQ, CHUNK, h=H, seed=1, mem_chunks=MEM, chunk_len=CHUNK)
+    q, k, v = q.to(dev), k.to(dev), v.to(dev)
+    ring = QuantKVRing(layers, 1, H, CHUNK, slots=MEM + 1, device=dev)
+    for mk, mv in mem:   # the same memory chunks in every layer
+        mk, mv = mk.to(dev), mv.to(dev)
+        for layer in range(layers):
+            ring.write(layer, mk, mv)
+        ring.commit()
+    del mem
+    kl = k.unsqueeze(0).expand(layers, *k.shape)
+    vl = v.unsqueeze(0).expand(layers, *v.shape)
+
+    def chunk():
+        for _ in range(passes):
+            for layer in range(layers):
+                ring.write(layer, k, v)
+                ring.attend(q, layer)
+        ring.write_layers(kl, vl)   # the clean pass's K/V saved for every layer at once
+
+    chunk()                          # warm-up: workspaces and the kernels' first launches
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        chunk()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / replays
+    calls = passes * layers
+    return {"calls": calls, "layers": layers, "passes": passes, "s_per_chunk": round(sec, 5),
+            "attention_TOPS": round(calls * attention_ops(LQ, LK) / sec / 1e12, 1), "hip_graph": True}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -156,6 +204,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU emulation baseline")
     ap.add_argument("--cpu-heads", type=int, default=3)
+    ap.add_argument("--no-sweep", action="store_true", help="skip the graph-captured per-chunk sweep")
     ap.add_argument("--only", choices=["attn", "requant", "copy"],
                     help="profiling run: after the set-up, launch only this part --steps times and print its "
                          "mean time (copy: a 2 GiB device-to-device copy, the byte-counter calibration)")
@@ -245,6 +294,7 @@ def main():
                     "GB/s": round(rq_gbps, 1), "frac_hbm": round(rq_gbps / HBM_PEAK_GBPS, 4),
                     "bytes_moved_two_v_planes": rq_moved},
     }
+    res["chunk_sweep"] = None if args.no_sweep else chunk_sweep(dev)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_heads)
     else:

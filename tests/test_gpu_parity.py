@@ -248,3 +248,50 @@ def test_reference_cosine_gate():
     e = (out - sd).abs()
     print(f"cosine vs fp32 SDPA {cos:.6f} (reference INT8: 0.999246); max {e.max():.3e} mean {e.mean():.3e}")
     assert cos >= 0.999246
+
+
+def test_graph_replay_matches_eager():
+    """The per-chunk path captured in a HIP graph (re-quant of the current chunk, Q quant, attention over a
+    memory ring, then a multi-layer save): every replay, with eager work and syncs in between, reproduces the eager
+    outputs bit for bit."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    layers, n, h = 2, 300, 4
+    q, k, v, mem = emu.make_inputs(n, n, h=h, seed=21, mem_chunks=2, chunk_len=n)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    ring = QuantKVRing(layers, 1, h, n, slots=4, device=DEV)
+    for mk, mv in mem:
+        for layer in range(layers):
+            ring.write(layer, mk.to(DEV), mv.to(DEV))
+        ring.commit()
+    outs = [torch.empty_like(q) for _ in range(2 * layers)]
+    kl, vl = k.unsqueeze(0).expand(layers, *k.shape), v.unsqueeze(0).expand(layers, *v.shape)
+
+    def chunk():
+        for p in range(2):
+            for layer in range(layers):
+                ring.write(layer, k, v)
+                outs[p * layers + layer].copy_(ring.attend(q, layer))
+        ring.write_layers(kl, vl)
+
+    chunk()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    k8_eager = ring.cache.k8.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        chunk()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        ring.cache.k8[:, ring.current].zero_()   # the slot the graph rewrites (the memory slots stay)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep} differs from the eager run"
+        assert torch.equal(ring.cache.k8[:, ring.current], k8_eager[:, ring.current])
+        chunk()   # eager work between replays
+        torch.cuda.synchronize()
