@@ -124,15 +124,17 @@ struct Piece {      // online-softmax state of one wave after a range of key blo
 // A workgroup is 8 waves x 32 queries = a 256-query tile. Waves 0-3 (group A) and 4-7 (group B) share the SIMDs
 // (one wave of each per SIMD) and run the same per-block program with a phase offset of one barrier: while one
 // group issues its MFMAs (S = K Q^T of block j, then P V of block j - 1) the other computes the softmax of its
-// block, so the matrix cores and the vector ALUs work at the same time. Group A also streams the K / V blocks
-// into LDS with direct global -> LDS loads, LEAD blocks ahead, through NSTAGE stages. Stage layout (24 KB):
+// block, so the matrix cores and the vector ALUs work at the same time. In its softmax phase every wave streams
+// one 1 KB piece of each tile of block j + LEAD into LDS with direct global -> LDS loads, through NSTAGE stages;
+// group A waits for its pieces at the end of a softmax phase, group B at the end of an MFMA phase, so each block
+// has landed before the barrier that opens its first MFMA phase. Stage layout (24 KB):
 // K tile 64 rows x 128 B, V tile 128 channels x 64 B, V residual tile; 16-byte chunks XOR-swizzled by row
 // (K: chunk ^ ((row >> 1) & 7), V: chunk ^ ((row >> 2) & 3)) so that the fragment reads of the MFMA operands hit
 // 16 distinct bank groups per 16 lanes, and every 1 KB of a tile is one contiguous DMA of 64 lanes x 16 B.
 constexpr int AT_WAVES = 8;
 constexpr int AT_THREADS = 64 * AT_WAVES;
-constexpr int NSTAGE = 5;
-constexpr int LEAD = 3;                        // NSTAGE - LEAD >= 2: a stage is free one phase before its reload
+constexpr int NSTAGE = 6;
+constexpr int LEAD = 4;                        // NSTAGE - LEAD >= 2: a stage is free one phase before its reload
 constexpr int ST_K = 0, ST_V = 8192, ST_VLO = 16384, ST_BYTES = 24576;
 static_assert(QT == 32 * AT_WAVES, "query tile");
 
@@ -147,12 +149,12 @@ __device__ __forceinline__ void phase_barrier() {
 // s_waitcnt on vmcnt only (lgkmcnt and expcnt at their maxima), for n < 16.
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
     case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
     case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // 0, and anything else: wait for everything
   }
 }
 
@@ -168,10 +170,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
                                              const uint8_t* __restrict__ v8, const uint8_t* __restrict__ v8lo,
                                              const float* __restrict__ v_scale, uint8_t* lds, int bh, int64_t q0,
                                              int j0, int j1, Piece& st) {
-  constexpr int NPB = TWO ? 6 : 4;   // DMA instructions per block of each loading wave
+  constexpr int NPB = TWO ? 3 : 2;   // DMA instructions per block of each wave
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform, so the loader's control stays scalar
-  const bool loader = w < 4;
+  const bool grp_a = w < 4;
   const int n = j1 - j0;
   v4i qf[4];
   {
@@ -200,14 +202,12 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     for (int h = 0; h < 2; ++h) vro[h] = ST_V + lq * 64 + (((2 * g + h) ^ s2) << 4);
   }
 
-  // loader (group A): wave wl = w moves 1 KB pieces 2 wl, 2 wl + 1 of each 8 KB tile
-  const int i0 = 2 * (w & 3);
-  int koff[2], voff[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int kr = 8 * (i0 + u) + (lane >> 3), vr = 16 * (i0 + u) + (lane >> 2);
-    koff[u] = kr * 128 + (((lane & 7) ^ ((kr >> 1) & 7)) << 4);
-    voff[u] = vr * 64 + (((lane & 3) ^ ((vr >> 2) & 3)) << 4);
+  // loader: wave w moves 1 KB piece w of each 8 KB tile (K, V and the V residual)
+  int koff, voff;
+  {
+    const int kr = 8 * w + (lane >> 3), vr = 16 * w + (lane >> 2);
+    koff = kr * 128 + (((lane & 7) ^ ((kr >> 1) & 7)) << 4);
+    voff = vr * 64 + (((lane & 3) ^ ((vr >> 2) & 3)) << 4);
   }
   // chunk lengths are only read when a cursor enters a chunk: an indexed read of the arguments is a memory load,
   // and waiting for it would also wait for every global -> LDS load in flight
@@ -226,13 +226,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   };
   seek(lc, lb);
   auto issue = [&](int stage) {
-    uint8_t* sb = lds + stage * ST_BYTES;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      dma16(kbase + koff[u], sb + ST_K + (i0 + u) * 1024);
-      dma16(vbase + voff[u], sb + ST_V + (i0 + u) * 1024);
-      if (TWO) dma16(vlbase + voff[u], sb + ST_VLO + (i0 + u) * 1024);
-    }
+    uint8_t* sb = lds + stage * ST_BYTES + w * 1024;
+    dma16(kbase + koff, sb + ST_K);
+    dma16(vbase + voff, sb + ST_V);
+    if (TWO) dma16(vlbase + voff, sb + ST_VLO);
   };
   auto advance = [&]() {
     if (--lrem == 0) {
@@ -259,58 +256,104 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int c_prev = c;
 
   const int npre = n < LEAD ? n : LEAD;
-  if (loader) {
-    for (int i = 0; i < npre; ++i) {
-      issue(i);
-      advance();
-    }
-    wait_vm(NPB * (npre - 1));   // the first block has landed
+  for (int i = 0; i < npre; ++i) {
+    issue(i);
+    advance();
   }
+  wait_vm(NPB * (npre - 1));   // every wave's piece of the first block has landed
   int ldstage = npre % NSTAGE;
   phase_barrier();
-  if (!loader) phase_barrier();   // group B runs one phase behind
+  if (!grp_a) phase_barrier();   // group B runs one phase behind
 
   v8i pb = {0, 0, 0, 0, 0, 0, 0, 0};
   int stage = 0, pstage = 0;
   for (int it = 0;; ++it) {
     // ---- MFMA phase: S of block it, P V of block it - 1 ----
     __builtin_amdgcn_s_setprio(1);
+    // LDS reads run ahead of the MFMAs that consume them: all eight K fragments and the first two V fragments
+    // are requested before the first QK MFMA, and each later pair of V fragments before the MFMA pair ahead of
+    // its consumers. The scheduling fences keep the compiler from sinking the reads next to their uses, which
+    // would expose the LDS latency once per MFMA.
     v16i acc[2];
-    if (it < n) {
-      const uint8_t* sk = lds + stage * ST_BYTES;
-      acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[0]), qf[0], magic, 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[0] + 4096), qf[0], magic, 0, 0, 0);
+    const uint8_t* sk = lds + stage * ST_BYTES;
+    const uint8_t* sv = lds + pstage * ST_BYTES;
+    constexpr int NVF = TWO ? 8 : 4;   // V fragments (one per PV MFMA): hi plane mt 0..3, then lo plane mt 0..3
+    auto vfrag = [&](int f) {
+      const int off = (f >= 4 ? ST_VLO - ST_V : 0) + (f & 3) * 2048;
+      const v4i lo = *(const v4i*)(sv + vro[0] + off);
+      const v4i hi = *(const v4i*)(sv + vro[1] + off);
+      const v8i r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      return r;
+    };
+    auto pv = [&](int f, const v8i& vf) {
+      if (f < 4)
+        st.o[f] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[f], 0, 0, 0, 0, 0, 0);
+      else   // residual plane, accumulated with block scale 2^-4
+        st.o[f & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[f & 3], 0, 0, 0, E8M0_LO, 0,
+                                                                      E8M0_ONE);
+    };
+    // Both halves run on every pass, so the LDS waits need no control-flow joins: at it == n the QK MFMAs read
+    // a stage nothing uses (its int32 results are dropped), and at it == 0 P is all zeros, so the PV MFMAs add
+    // exactly 0 (stage 0 holds block 0, whose fp8 V values are finite).
+    constexpr bool do_qk = true, do_pv = true;
+    // Nothing is outstanding on the LDS / scalar counter here in the common case; saying so lets the waits
+    // below count individual LDS reads (a scalar load that might still be pending forces every wait to zero).
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt and expcnt unconstrained
+    v4i kf[8];
+    v8i vq[2];
+    if (do_qk) {
 #pragma unroll
-      for (int kk = 1; kk < 4; ++kk) {
-        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[kk]), qf[kk], acc[0], 0, 0, 0);
-        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + kro[kk] + 4096), qf[kk], acc[1], 0, 0, 0);
+      for (int kk = 0; kk < 4; ++kk) {
+        kf[2 * kk] = *(const v4i*)(sk + kro[kk]);
+        kf[2 * kk + 1] = *(const v4i*)(sk + kro[kk] + 4096);
       }
     }
-    if (it > 0) {
-      const uint8_t* sv = lds + pstage * ST_BYTES;
+    if (do_pv) {
+      vq[0] = vfrag(0);
+      vq[1] = vfrag(1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (do_qk) {
+      acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0], qf[0], magic, 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1], qf[0], magic, 0, 0, 0);
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const v4i lo = *(const v4i*)(sv + vro[0] + mt * 2048);
-        const v4i hi = *(const v4i*)(sv + vro[1] + mt * 2048);
-        const v8i vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[mt], 0, 0, 0, 0, 0, 0);
+      for (int kk = 1; kk < 4; ++kk) {
+        acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[2 * kk], qf[kk], acc[0], 0, 0, 0);
+        acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[2 * kk + 1], qf[kk], acc[1], 0, 0, 0);
       }
-      if (TWO) {   // residual plane, accumulated with block scale 2^-4
+      // MFMAs are pure register operations: without this the compiler sinks them below the phase barrier,
+      // next to their first use in the softmax, and the two halves' MFMA and softmax phases no longer alternate
+      asm volatile("" : "+v"(acc[0]), "+v"(acc[1]));
+    }
+    if (do_pv) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          const v4i lo = *(const v4i*)(sv + vro[0] + (ST_VLO - ST_V) + mt * 2048);
-          const v4i hi = *(const v4i*)(sv + vro[1] + (ST_VLO - ST_V) + mt * 2048);
-          const v8i vl = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          st.o[mt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vl, pb, st.o[mt], 0, 0, 0, E8M0_LO, 0, E8M0_ONE);
+      for (int f = 0; f < NVF; f += 2) {
+        v8i nx[2];
+        if (f + 2 < NVF) {
+          nx[0] = vfrag(f + 2);
+          nx[1] = vfrag(f + 3);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        pv(f, vq[0]);
+        pv(f + 1, vq[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (f + 2 < NVF) {
+          vq[0] = nx[0];
+          vq[1] = nx[1];
         }
       }
+      asm volatile("" : "+v"(st.o[0]), "+v"(st.o[1]), "+v"(st.o[2]), "+v"(st.o[3]));   // as for acc
     }
     __builtin_amdgcn_s_setprio(0);
     if (it == n) break;
+    if (!grp_a) {   // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD - 1 in flight)
+      const int ahead = (it + LEAD - 1 < n ? it + LEAD - 1 : n - 1) - (it + 1);
+      wait_vm(ahead > 0 ? NPB * ahead : 0);
+    }
     phase_barrier();
 
     // ---- softmax phase for block it (chunk c, block blk); group A streams block it + LEAD ----
-    if (loader && it + LEAD < n) {
+    if (it + LEAD < n) {
       issue(ldstage);
       advance();
       ldstage = ldstage + 1 == NSTAGE ? 0 : ldstage + 1;
@@ -330,11 +373,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       c_prev = c;
     }
     float ks;
-    {   // the block's K scale through a provably uniform address: a scalar load
+    {   // the block's K scale through a uniform constant-address-space pointer: a scalar load. A generic or
+        // global pointer gives a vector load, and waiting for it would also wait for every global -> LDS
+        // load in flight, the prefetch of the coming blocks included.
       const uint64_t ka = (uint64_t)ksp;
       const uint64_t ku = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(ka >> 32)) << 32) |
                           (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ka);
-      ks = *(const float*)ku;
+      ks = *(const __attribute__((address_space(4))) float*)ku;
     }
     const float cb = qs_sl2 * ks;
     int si[32];
@@ -386,7 +431,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       ++blk;
       ++ksp;
     }
-    if (loader) {   // block it + 1 has landed (blocks up to it + LEAD may still be in flight)
+    if (grp_a) {   // A's pieces of block it + 1 have landed (blocks up to it + LEAD may still be in flight)
       const int ahead = (it + LEAD < n ? it + LEAD : n - 1) - (it + 1);
       wait_vm(ahead > 0 ? NPB * ahead : 0);
     }
@@ -394,7 +439,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     pstage = stage;
     stage = stage + 1 == NSTAGE ? 0 : stage + 1;
   }
-  if (loader) phase_barrier();   // matches group B's extra barrier at the start
+  if (grp_a) phase_barrier();   // matches group B's extra barrier at the start
   phase_barrier();               // every wave is done with the stages before they are refilled
   st.m = m_ref;
   st.l = halves_sum(l_run);
