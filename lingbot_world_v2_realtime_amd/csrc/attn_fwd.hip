@@ -137,6 +137,14 @@ constexpr int NSTAGE = 6;
 constexpr int LEAD = 4;                        // NSTAGE - LEAD >= 2: a stage is free one phase before its reload
 constexpr int ST_K = 0, ST_V = 8192, ST_VLO = 16384, ST_BYTES = 24576;
 static_assert(QT == 32 * AT_WAVES, "query tile");
+// Per-piece chunk tables after the stages, so a chunk switch inside the loop reads LDS instead of global
+// memory (waiting for a global load would also wait for every global -> LDS load in flight):
+//   ratio [chunk c][channel]  v_scale(c - 1) / v_scale(c), the factor that takes O to chunk c's V scale
+//   bias  [chunk c][query]    q . mean_k(c) * sm_scale * log2(e) of the tile's queries
+constexpr int TAB_RATIO = NSTAGE * ST_BYTES;
+constexpr int TAB_BIAS = TAB_RATIO + LBW_MAX_SEGMENTS * D * 4;
+constexpr int AT_LDS = TAB_BIAS + LBW_MAX_SEGMENTS * QT * 4;   // 159744 of the 163840 bytes of a CU
+static_assert(AT_LDS <= 163840, "LDS");
 
 // Workgroup barrier that also stops the compiler from moving memory accesses across it. No wait is implied:
 // the global -> LDS loads a phase depends on are waited for explicitly by the waves that issued them.
@@ -153,7 +161,9 @@ __device__ __forceinline__ void wait_vm(int n) {
     case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
     case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
     case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
     case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // 0, and anything else: wait for everything
   }
 }
@@ -252,13 +262,49 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int crem = a.seg_blk0[c + 1] - j0;                   // blocks left in chunk c, this one included
   int last_valid = a.seg_len[c] - (a.seg_blk0[c + 1] - a.seg_blk0[c] - 1) * KB;   // keys in its last block
   const float* ksp = k_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * a.nbc + blk;
-  float beta = multi ? bias[((int64_t)c * a.bh + bh) * a.lp + q0 + lq] * a.sl2 : 0.f;
   int c_prev = c;
+
+  // chunk tables: their global loads go out before the first blocks' DMA, so waiting for them waits for
+  // nothing else. The previous piece's readers are done: it ended with a workgroup barrier.
+  float* const ratio_tab = (float*)(lds + TAB_RATIO);
+  float* const bias_tab = (float*)(lds + TAB_BIAS) + 32 * w + lq;   // this lane's query; [c * QT]
+  float tb[LBW_MAX_SEGMENTS], rnum[2], rden[2];
+  if (multi) {
+#pragma unroll
+    for (int cc = 0; cc < LBW_MAX_SEGMENTS; ++cc)
+      if (cc < a.n_seg) tb[cc] = bias[((int64_t)cc * a.bh + bh) * a.lp + q0 + lq];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int idx = t + AT_THREADS * r, cc = 1 + (idx >> 7), ch = idx & (D - 1);
+      if (cc < a.n_seg) {
+        rnum[r] = v_scale[((int64_t)a.seg_slot[cc - 1] * a.bh + bh) * D + ch];
+        rden[r] = v_scale[((int64_t)a.seg_slot[cc] * a.bh + bh) * D + ch];
+      }
+    }
+  }
 
   const int npre = n < LEAD ? n : LEAD;
   for (int i = 0; i < npre; ++i) {
     issue(i);
     advance();
+  }
+  float beta = 0.f;
+  if (multi) {
+    wait_vm(NPB * npre);   // the table loads (older than every DMA) have landed
+#pragma unroll
+    for (int cc = 0; cc < LBW_MAX_SEGMENTS; ++cc)
+      if (cc < a.n_seg) bias_tab[cc * QT] = tb[cc] * a.sl2;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int idx = t + AT_THREADS * r, cc = 1 + (idx >> 7);
+      if (cc < a.n_seg) ratio_tab[idx + D] = rnum[r] / rden[r];   // [cc][ch] = [(cc - 1) * D + ch + D]
+    }
+    beta = tb[0];
+#pragma unroll
+    for (int cc = 1; cc < LBW_MAX_SEGMENTS; ++cc)
+      if (cc == c) beta = tb[cc];
+    beta *= a.sl2;
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the table writes are done before the barrier below
   }
   wait_vm(NPB * (npre - 1));   // every wave's piece of the first block has landed
   int ldstage = npre % NSTAGE;
@@ -359,17 +405,20 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       ldstage = ldstage + 1 == NSTAGE ? 0 : ldstage + 1;
     }
     if (c != c_prev) {
-      // a new chunk: O (blocks before this one) to its V scale, and its logit bias
-      const float* vs_old = v_scale + ((int64_t)a.seg_slot[c_prev] * a.bh + bh) * D;
-      const float* vs_new = v_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * D;
+      // a new chunk (c_prev == c - 1: every chunk has a block): O (blocks before this one) to its V scale,
+      // and its logit bias, both from the piece's LDS tables
+      const float* rt = ratio_tab + c * D + 4 * g;
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int ch = 32 * mt + 8 * (i >> 2) + 4 * g + (i & 3);
-          st.o[mt][i] *= vs_old[ch] / vs_new[ch];
+        for (int q = 0; q < 4; ++q) {   // channels 32 mt + 8 q + 4 g + (0..3)
+          const float4 r = *(const float4*)(rt + 32 * mt + 8 * q);
+          st.o[mt][4 * q] *= r.x;
+          st.o[mt][4 * q + 1] *= r.y;
+          st.o[mt][4 * q + 2] *= r.z;
+          st.o[mt][4 * q + 3] *= r.w;
         }
-      beta = bias[((int64_t)c * a.bh + bh) * a.lp + q0 + lq] * a.sl2;
+      beta = bias_tab[c * QT];
       c_prev = c;
     }
     float ks;
@@ -503,7 +552,7 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* _
                                                                  const float* __restrict__ v_scale,
                                                                  uint16_t* __restrict__ out, float* __restrict__ o_part,
                                                                  float* __restrict__ ml_part, AttnArgs a) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NSTAGE * ST_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[AT_LDS];
   const int gid = blockIdx.x, x = gid % XCDS, i = gid / XCDS;
   const int w = threadIdx.x >> 6;
   const XcdPlan p = xcd_plan(a, x);
