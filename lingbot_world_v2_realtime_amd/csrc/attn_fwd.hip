@@ -124,7 +124,7 @@ struct Piece {      // online-softmax state of one wave after a range of key blo
 // A workgroup is 8 waves x 32 queries = a 256-query tile. Waves 0-3 (group A) and 4-7 (group B) share the SIMDs
 // (one wave of each per SIMD) and run the same per-block program with a phase offset of one barrier: while one
 // group issues its MFMAs (S = K Q^T of block j, then P V of block j - 1) the other computes the softmax of its
-// block, so the matrix cores and the vector ALUs work at the same time. In its softmax phase every wave streams
+// block, so the matrix cores and the vector ALUs work at the same time. In its MFMA phase every wave streams
 // one 1 KB piece of each tile of block j + LEAD into LDS with direct global -> LDS loads, through NSTAGE stages;
 // group A waits for its pieces at the end of a softmax phase, group B at the end of an MFMA phase, so each block
 // has landed before the barrier that opens its first MFMA phase. Stage layout (24 KB):
@@ -359,6 +359,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       vq[1] = vfrag(1);
     }
     __builtin_amdgcn_sched_barrier(0);
+    // DMA of block it + LEAD into the stage of block it - 2 (both groups finished it a phase ago); issued here,
+    // where the wave mostly waits for its LDS reads and the matrix core, instead of in the softmax phase
+    if (it + LEAD < n) {
+      issue(ldstage);
+      advance();
+      ldstage = ldstage + 1 == NSTAGE ? 0 : ldstage + 1;
+    }
     if (do_qk) {
       acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0], qf[0], magic, 0, 0, 0);
       acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1], qf[0], magic, 0, 0, 0);
@@ -392,18 +399,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     }
     __builtin_amdgcn_s_setprio(0);
     if (it == n) break;
-    if (!grp_a) {   // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD - 1 in flight)
-      const int ahead = (it + LEAD - 1 < n ? it + LEAD - 1 : n - 1) - (it + 1);
+    if (!grp_a) {   // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD in flight)
+      const int ahead = (it + LEAD < n ? it + LEAD : n - 1) - (it + 1);
       wait_vm(ahead > 0 ? NPB * ahead : 0);
     }
     phase_barrier();
 
-    // ---- softmax phase for block it (chunk c, block blk); group A streams block it + LEAD ----
-    if (it + LEAD < n) {
-      issue(ldstage);
-      advance();
-      ldstage = ldstage + 1 == NSTAGE ? 0 : ldstage + 1;
-    }
+    // ---- softmax phase for block it (chunk c, block blk) ----
     if (c != c_prev) {
       // a new chunk (c_prev == c - 1: every chunk has a block): O (blocks before this one) to its V scale,
       // and its logit bias, both from the piece's LDS tables
