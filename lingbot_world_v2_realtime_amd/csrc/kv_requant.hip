@@ -3,8 +3,8 @@
 // Three launches:
 //   1. kv_stats:    per 64-token block (grid: block, batch*head, layer), fp32 column sums of K and column max |V|
 //                   (K and V read once).
-//   2. kv_finalize: per (batch*head, layer), all of the group's block partials loaded at once, then the
-//                   fixed-order mean -> bf16, the V scale and its reciprocal.
+//   2. kv_finalize: per (batch*head, layer), the block partials summed into 4-block super-blocks in parallel,
+//                   the super-blocks left to right, then the mean -> bf16, the V scale and its reciprocal.
 //   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * (448 / amax) -> e4m3 hi = rn(y) and, when a
 //                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K and
 //                   V a second time).
