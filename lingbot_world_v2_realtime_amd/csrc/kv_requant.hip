@@ -3,8 +3,9 @@
 // Three launches:
 //   1. kv_stats:    per 64-token block (grid: block, batch*head, layer), fp32 column sums of K and column max |V|
 //                   (K and V read once).
-//   2. kv_finalize: per (batch*head, layer), the block partials summed into 4-block super-blocks in parallel,
-//                   the super-blocks left to right, then the mean -> bf16, the V scale and its reciprocal.
+//   2. kv_finalize: per (batch*head, layer, 16 channels), the block partials summed into 4-block super-blocks
+//                   in parallel, the super-blocks left to right, then the mean -> bf16, the V scale and its
+//                   reciprocal.
 //   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * (448 / amax) -> e4m3 hi = rn(y) and, when a
 //                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K and
 //                   V a second time).
@@ -24,7 +25,7 @@ struct ReqArgs {
 };
 
 constexpr int REQ_SUPER = 4;   // blocks per super-block of the mean's defined order
-constexpr int FIN_U = 32;      // super-block sums the finaliser holds in LDS at a time
+constexpr int FIN_U = 8;       // super-block sums per lane the finaliser holds in LDS at a time
 
 // Thread (cg, q) = (t & 15, t >> 4) sums channels 8 cg .. + 8 over tokens 4 q .. 4 q + 3 of the block.
 __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restrict__ k,
@@ -79,54 +80,52 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
   }
 }
 
-// One workgroup per (batch*head, layer). Super-block sums U[u] = B[4u] + .. + B[4u+3] are formed in parallel
-// (thread t: channel t & 127, super-blocks t >> 7, + 2, ..), then summed left to right per channel.
+// One workgroup per (batch*head, layer, group of 16 channels). Thread (j, c) = (t >> 4, t & 15) forms the
+// super-block sums U[u] = B[4u] + .. + B[4u+3] of channel 16 cgrp + c for u = j, j + 16, .. (all of them at
+// once, in parallel), and the maxima; then one thread per channel sums the U left to right.
+constexpr int FIN_CH = 16;                 // channels per finaliser workgroup
+constexpr int FIN_J = 256 / FIN_CH;        // super-block lanes per channel
 __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float* __restrict__ part_sum,
                                                           const float* __restrict__ part_amax,
                                                           float* __restrict__ v_recip, float* __restrict__ km,
                                                           float* __restrict__ v_scale) {
-  __shared__ float buf[FIN_U * D];
-  __shared__ float fin[D];
-  const int bh = blockIdx.x, layer = blockIdx.y;
-  const int t = threadIdx.x, c = t & (D - 1), half = t >> 7;
+  __shared__ float buf[FIN_U * FIN_J * FIN_CH];
+  __shared__ float s_mx[FIN_J][FIN_CH];
+  const int bh = blockIdx.x, layer = blockIdx.y, cgrp = blockIdx.z;
+  const int t = threadIdx.x, c = t & (FIN_CH - 1), j = t / FIN_CH, ch = cgrp * FIN_CH + c;
   const int64_t grp = (int64_t)layer * a.bh + bh;
-  const float* bsum = part_sum + grp * a.nb * D + c;
-  const float* bmax = part_amax + grp * a.nb * D + c;
+  const float* bsum = part_sum + grp * a.nb * D + ch;
+  const float* bmax = part_amax + grp * a.nb * D + ch;
   const int nsup = (int)((a.nb + REQ_SUPER - 1) / REQ_SUPER);
   float tot = 0.f, mx = 0.f;
-  for (int u0 = 0; u0 < nsup; u0 += FIN_U) {
-    const int nu = min(FIN_U, nsup - u0);
-#pragma unroll 4
-    for (int uu = half; uu < nu; uu += 2) {
+  for (int u0 = 0; u0 < nsup; u0 += FIN_U * FIN_J) {
+    const int nu = min(FIN_U * FIN_J, nsup - u0);
+    for (int uu = j; uu < nu; uu += FIN_J) {
       const int b0 = (u0 + uu) * REQ_SUPER;
-      float bs[REQ_SUPER], bm[REQ_SUPER];
-#pragma unroll
-      for (int i = 0; i < REQ_SUPER; ++i) {
-        const bool ok = b0 + i < a.nb;
-        bs[i] = ok ? bsum[(int64_t)(b0 + i) * D] : 0.f;
-        bm[i] = ok ? bmax[(int64_t)(b0 + i) * D] : 0.f;
-      }
       float us = 0.f;   // absent blocks add +0, which leaves the sum unchanged
 #pragma unroll
       for (int i = 0; i < REQ_SUPER; ++i) {
-        us = __fadd_rn(us, bs[i]);
-        mx = fmaxf(mx, bm[i]);
+        const bool ok = b0 + i < a.nb;
+        us = __fadd_rn(us, ok ? bsum[(int64_t)(b0 + i) * D] : 0.f);
+        mx = fmaxf(mx, ok ? bmax[(int64_t)(b0 + i) * D] : 0.f);
       }
-      buf[uu * D + c] = us;
+      buf[uu * FIN_CH + c] = us;
     }
     __syncthreads();
-    if (t < D)
-      for (int uu = 0; uu < nu; ++uu) tot = __fadd_rn(tot, buf[uu * D + c]);
+    if (j == 0)
+      for (int uu = 0; uu < nu; ++uu) tot = __fadd_rn(tot, buf[uu * FIN_CH + c]);
     __syncthreads();
   }
-  if (t >= D) fin[c] = mx;
+  s_mx[j][c] = mx;
   __syncthreads();
-  if (t < D) {
-    mx = fmaxf(fmaxf(mx, fin[c]), AMAX_FLOOR);
-    const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + c;
+  if (j == 0) {
+#pragma unroll
+    for (int jj = 1; jj < FIN_J; ++jj) mx = fmaxf(mx, s_mx[jj][c]);
+    mx = fmaxf(mx, AMAX_FLOOR);
+    const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + ch;
     km[so] = bf16_round(__fdiv_rn(tot, (float)a.len));
     v_scale[so] = __fdiv_rn(mx, V_MAX);
-    v_recip[grp * D + c] = __fdiv_rn(V_MAX, mx);
+    v_recip[grp * D + ch] = __fdiv_rn(V_MAX, mx);
   }
 }
 
@@ -264,7 +263,8 @@ extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t laye
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
   hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
-  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers), dim3(256), 0, st, a, part_sum,
+  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers, D / FIN_CH), dim3(256), 0, st, a,
+                     part_sum,
                      part_amax, v_recip, km, v_scale);
   hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
