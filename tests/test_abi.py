@@ -53,9 +53,10 @@ def test_status_strings_and_version(lib):
 
 
 def test_requant_workspace_formula(lib):
-    for layers, bh, n in ((1, 1, 1), (30, 24, 1508), (2, 3, 64), (1, 5, 65)):
+    for layers, bh, n in ((1, 1, 1), (30, 24, 1508), (2, 3, 64), (1, 5, 65), (30, 12, 6032), (1, 1, 262400)):
         nb = -(-n // 64)
         g = layers * bh
+        # per-block column sums and maxima, plus the per-channel V reciprocals
         assert lib.lbw_kv_requant_workspace_bytes(layers, bh, n) == (2 * g * nb * 128 + g * 128) * 4
     assert lib.lbw_kv_requant_workspace_bytes(0, 1, 1) == 0
 

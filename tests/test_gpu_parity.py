@@ -46,6 +46,20 @@ def test_requant_bit_exact(n):
     _check_chunk(ring, 0, 1, emu.requant(k, v), n)
 
 
+@pytest.mark.parametrize("layers,n", [(3, 65536), (1, 262400)])
+def test_requant_long_chunks(layers, n):
+    """Long chunks, bit-exact: 65536 tokens (1024 blocks, 256 four-block super-blocks) in 3 layers, and 262400
+    tokens (4100 blocks: the finaliser's super-block sums go through its LDS buffer in 9 passes)."""
+    torch.manual_seed(n)
+    k = (torch.randn(layers, 1, n, 1, 128) + 3 * torch.randn(layers, 1, 1, 1, 128)).to(torch.bfloat16)
+    v = (torch.randn(layers, 1, n, 1, 128) * 1.7).to(torch.bfloat16)
+    ring = _ring(layers, 1, n, slots=1)
+    _k().kv_requant(k.to(DEV), v.to(DEV), ring, slot=0)
+    torch.cuda.synchronize()
+    for l in range(layers):
+        _check_chunk(ring, l, 0, emu.requant(k[l], v[l]), n)
+
+
 def test_requant_cfg1_shape_and_zero_chunk():
     q, k, v, _ = emu.make_inputs(1508, 1508)
     ring = _ring(1, 12, 1508)
@@ -77,8 +91,8 @@ def test_requant_layers_and_strides():
 
 
 def test_requant_30_layers():
-    """The bench shape: 30 layers x 12 heads x 6032 tokens in one call (360 (layer, head) groups, launched as
-    stats / quant pairs over groups of layers), sampled layers bit-exact, also on a second call into the same
+    """The bench shape: 30 layers x 12 heads x 6032 tokens in one call (360 (layer, head) chunks in one
+    statistics / finalise / quantise sequence), sampled layers bit-exact, also on a second call into the same
     workspace."""
     layers, h, n = 30, 12, 6032
     g = torch.Generator(device=DEV).manual_seed(30)
