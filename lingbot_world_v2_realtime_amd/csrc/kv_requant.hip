@@ -130,7 +130,9 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
 }
 
 // Thread t owns channels 8*(t & 15) .. +8 and the 4 consecutive keys 4*(t >> 4) .. +4 of the block, so its
-// e4m3 V bytes for one channel are 4 adjacent positions (one dword) of the permuted layout.
+// e4m3 V bytes for one channel are 4 adjacent positions (one dword) of the permuted layout. Layers go last to
+// first: the statistics pass read the last layers most recently, so the first re-reads can still find them in
+// the memory-side cache.
 __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, ReqArgs a,
                                                        const float* __restrict__ v_recip,
@@ -139,7 +141,7 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
                                                        uint8_t* __restrict__ v8, uint8_t* __restrict__ v8lo) {
   __shared__ uint32_t s_v[2][D * 16];   // hi / lo planes: [channel][16 dwords], dword xor-swizzled by channel >> 3
   __shared__ float s_red[4];
-  const int blk = blockIdx.x, bh = blockIdx.y, layer = blockIdx.z;
+  const int blk = blockIdx.x, bh = blockIdx.y, layer = gridDim.z - 1 - blockIdx.z;
   const int t = threadIdx.x, cg = t & 15, kq = t >> 4;
   const int64_t b = bh / a.heads, h = bh % a.heads;
   const uint16_t* kp = k + layer * a.k_sl + b * a.k_sb + h * a.k_sh + cg * 8;
