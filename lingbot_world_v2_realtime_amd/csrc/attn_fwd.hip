@@ -143,7 +143,10 @@ static_assert(QT == 32 * AT_WAVES, "query tile");
 //   bias  [chunk c][query]    q . mean_k(c) * sm_scale * log2(e) of the tile's queries
 constexpr int TAB_RATIO = NSTAGE * ST_BYTES;
 constexpr int TAB_BIAS = TAB_RATIO + LBW_MAX_SEGMENTS * D * 4;
-constexpr int AT_LDS = TAB_BIAS + LBW_MAX_SEGMENTS * QT * 4;   // 159744 of the 163840 bytes of a CU
+// K scale of the block in each stage, one copy per wave ([stage][wave]): it arrives by DMA with the block's
+// tiles, so the softmax reads it from LDS instead of waiting for a scalar load per block
+constexpr int TAB_KS = TAB_BIAS + LBW_MAX_SEGMENTS * QT * 4;
+constexpr int AT_LDS = TAB_KS + NSTAGE * AT_WAVES * 4;   // 159936 of the 163840 bytes of a CU
 static_assert(AT_LDS <= 163840, "LDS");
 
 // Workgroup barrier that also stops the compiler from moving memory accesses across it. No wait is implied:
@@ -154,7 +157,7 @@ __device__ __forceinline__ void phase_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// s_waitcnt on vmcnt only (lgkmcnt and expcnt at their maxima), for n < 16.
+// s_waitcnt on vmcnt only (lgkmcnt and expcnt at their maxima); vmcnt bits 5:4 sit in bits 15:14.
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
     case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
@@ -164,12 +167,17 @@ __device__ __forceinline__ void wait_vm(int n) {
     case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
     case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
     case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+    case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
     default: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // 0, and anything else: wait for everything
   }
 }
 
 __device__ __forceinline__ void dma16(const void* src, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+__device__ __forceinline__ void dma4(const void* src, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
@@ -180,7 +188,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
                                              const uint8_t* __restrict__ v8, const uint8_t* __restrict__ v8lo,
                                              const float* __restrict__ v_scale, uint8_t* lds, int bh, int64_t q0,
                                              int j0, int j1, Piece& st) {
-  constexpr int NPB = TWO ? 3 : 2;   // DMA instructions per block of each wave
+  constexpr int NPB = TWO ? 4 : 3;   // DMA instructions per block of each wave (tiles + the K scale)
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform, so the loader's control stays scalar
   const bool grp_a = w < 4;
@@ -228,11 +236,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   const int8_t* kbase;
   const uint8_t* vbase;
   const uint8_t* vlbase;
+  const float* ksbase;
   auto seek = [&](int cc, int bb) {
     const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
     kbase = k8 + (sbh * a.cap + (int64_t)bb * KB) * D;
     vbase = v8 + (sbh * a.nbc + bb) * TILE_BYTES;
     if (TWO) vlbase = v8lo + (sbh * a.nbc + bb) * TILE_BYTES;
+    ksbase = k_scale + sbh * a.nbc + bb;
   };
   seek(lc, lb);
   auto issue = [&](int stage) {
@@ -240,6 +250,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     dma16(kbase + koff, sb + ST_K);
     dma16(vbase + voff, sb + ST_V);
     if (TWO) dma16(vlbase + voff, sb + ST_VLO);
+    if (lane == 0) dma4(ksbase, lds + TAB_KS + (stage * AT_WAVES + w) * 4);   // one lane: 4 bytes
   };
   auto advance = [&]() {
     if (--lrem == 0) {
@@ -252,6 +263,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       kbase += TILE_BYTES;
       vbase += TILE_BYTES;
       if (TWO) vlbase += TILE_BYTES;
+      ++ksbase;
     }
   };
 
@@ -261,7 +273,6 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int blk = j0 - a.seg_blk0[c];
   int crem = a.seg_blk0[c + 1] - j0;                   // blocks left in chunk c, this one included
   int last_valid = a.seg_len[c] - (a.seg_blk0[c + 1] - a.seg_blk0[c] - 1) * KB;   // keys in its last block
-  const float* ksp = k_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * a.nbc + blk;
   int c_prev = c;
 
   // chunk tables: their global loads go out before the first blocks' DMA, so waiting for them waits for
@@ -354,6 +365,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
         kf[2 * kk + 1] = *(const v4i*)(sk + kro[kk] + 4096);
       }
     }
+    // the K scale of block it, for its softmax in the next phase (this wave's copy landed with its pieces)
+    const float ks = *(const float*)(lds + TAB_KS + (stage * AT_WAVES + w) * 4);
     if (do_pv) {
       vq[0] = vfrag(0);
       vq[1] = vfrag(1);
@@ -400,8 +413,12 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     __builtin_amdgcn_s_setprio(0);
     if (it == n) break;
     if (!grp_a) {   // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD in flight)
-      const int ahead = (it + LEAD < n ? it + LEAD : n - 1) - (it + 1);
-      wait_vm(ahead > 0 ? NPB * ahead : 0);
+      if (it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
+        wait_vm(NPB * (LEAD - 1));
+      } else {
+        const int ahead = n - 1 - (it + 1);
+        wait_vm(ahead > 0 ? NPB * ahead : 0);
+      }
     }
     phase_barrier();
 
@@ -422,15 +439,6 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
         }
       beta = bias_tab[c * QT];
       c_prev = c;
-    }
-    float ks;
-    {   // the block's K scale through a uniform constant-address-space pointer: a scalar load. A generic or
-        // global pointer gives a vector load, and waiting for it would also wait for every global -> LDS
-        // load in flight, the prefetch of the coming blocks included.
-      const uint64_t ka = (uint64_t)ksp;
-      const uint64_t ku = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(ka >> 32)) << 32) |
-                          (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ka);
-      ks = *(const __attribute__((address_space(4))) float*)ku;
     }
     const float cb = qs_sl2 * ks;
     int si[32];
@@ -477,14 +485,16 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       blk = 0;
       crem = a.seg_blk0[c + 1] - a.seg_blk0[c];
       last_valid = a.seg_len[c] - (crem - 1) * KB;
-      ksp = k_scale + ((int64_t)a.seg_slot[c] * a.bh + bh) * a.nbc;
     } else {
       ++blk;
-      ++ksp;
     }
     if (grp_a) {   // A's pieces of block it + 1 have landed (blocks up to it + LEAD may still be in flight)
-      const int ahead = (it + LEAD < n ? it + LEAD : n - 1) - (it + 1);
-      wait_vm(ahead > 0 ? NPB * ahead : 0);
+      if (it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
+        wait_vm(NPB * (LEAD - 1));
+      } else {
+        const int ahead = n - 1 - (it + 1);
+        wait_vm(ahead > 0 ? NPB * ahead : 0);
+      }
     }
     phase_barrier();
     pstage = stage;
