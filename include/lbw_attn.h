@@ -83,7 +83,8 @@ int lbw_kv_requant(const uint16_t* k, const uint16_t* v,
  * Quantise bf16 Q [batch][lq][heads][128] (strides s_batch, s_tok, s_head) to int8 with one scale per
  * 32 rows (Sage per_warp_int8 Q part with BLKQ=128, WARPQ=32: lingbot/layers/sage_preq.py:116,
  * experiments/modules/sage_kvq.py:104). When n_seg > 1 it also writes bias[c][bh][row] = q . km of chunk
- * seg_slot[c] of the (layer-offset) cache `km` with `slots` slots. seg_slot is a host array.
+ * seg_slot[c] of the (layer-offset) cache `km` with `slots` slots; km is then 16-byte aligned. seg_slot is a
+ * host array.
  */
 int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
                 int64_t s_batch, int64_t s_tok, int64_t s_head,

@@ -15,12 +15,21 @@ struct QArgs {
 __global__ __launch_bounds__(64) void quant_q_kernel(const uint16_t* __restrict__ q, QArgs a,
                                                      int8_t* __restrict__ q8, float* __restrict__ q_scale,
                                                      const float* __restrict__ km, float* __restrict__ bias) {
+  __shared__ __align__(16) float s_km[LBW_MAX_SEGMENTS][D];   // the chunks' K means for the logit bias
   const int grp = blockIdx.x, bh = blockIdx.y;
   const int lane = threadIdx.x, r = lane >> 1, half = lane & 1;
   const int64_t row = (int64_t)grp * QG + r;
   const int64_t b = bh / a.heads, h = bh % a.heads;
   const bool ok = row < a.lq;
   const uint16_t* qp = q + b * a.sb + row * a.st + h * a.sh + half * 64;
+  // the K means go through LDS once per row group: read from global memory inside the dot products below,
+  // every lane would wait on 16 dependent loads per chunk
+  if (a.n_seg > 1) {
+    for (int i = lane; i < a.n_seg * (D / 4); i += 64) {
+      const int c = i / (D / 4), k4 = i % (D / 4);
+      *(float4*)&s_km[c][4 * k4] = *(const float4*)(km + ((int64_t)a.seg_slot[c] * a.bh + bh) * D + 4 * k4);
+    }
+  }
   float x[64];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -47,8 +56,9 @@ __global__ __launch_bounds__(64) void quant_q_kernel(const uint16_t* __restrict_
     *(v4i*)(out + 16 * i) = v4i{w[0], w[1], w[2], w[3]};
   }
   if (a.n_seg > 1) {
+    __syncthreads();   // s_km is filled (one wave: orders the LDS writes before the reads)
     for (int c = 0; c < a.n_seg; ++c) {
-      const float* m = km + ((int64_t)a.seg_slot[c] * a.bh + bh) * D + half * 64;
+      const float* m = &s_km[c][half * 64];
       float acc = 0.f;
 #pragma unroll
       for (int i = 0; i < 64; ++i) acc = fmaf(x[i], m[i], acc);
@@ -81,6 +91,7 @@ extern "C" int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t
   for (int c = 0; c < LBW_MAX_SEGMENTS; ++c) a.seg_slot[c] = 0;
   if (n_seg > 1) {
     if (!km || !bias || !seg_slot) return LBW_E_NULL;
+    if ((uintptr_t)km & 15) return LBW_E_ALIGN;   // read as float4
     for (int c = 0; c < n_seg; ++c) {
       if (seg_slot[c] < 0 || seg_slot[c] >= slots) return LBW_E_SEGMENTS;
       a.seg_slot[c] = seg_slot[c];

@@ -100,6 +100,7 @@ def test_quant_q_argument_checks(lib):
     assert quant_q(lib, st=(0, 256, 12)) == E_ALIGN
     assert quant_q(lib, n_seg=2, seg=None) == E_NULL
     assert quant_q(lib, n_seg=2, seg=seg) == E_SEGMENTS   # slot 5 of a 4-slot cache
+    assert quant_q(lib, n_seg=2, seg=seg, km=FAKE + 4) == E_ALIGN   # the K means are read as float4
 
 
 def attn(lib, **kw):
