@@ -168,6 +168,37 @@ def test_attention_small_vs_oracle(lq, lk):
     assert err_sdpa.mean() <= 1.1 * err_scheme.mean() + 1e-5
 
 
+def test_batch_two():
+    """Batch 2 (batch * heads rows of every buffer): each batch element's int8 K / V / Q, scales and means are
+    the oracle's for that element alone, bit for bit, and its attention output is as close to the oracle and
+    to fp32 SDPA as a batch-1 call."""
+    lq, lk, h = 300, 700, 3
+    ins = [emu.make_inputs(lq, lk, h=h, seed=40 + i) for i in range(2)]
+    q, k, v = (torch.cat([x[j] for x in ins]) for j in range(3))   # [2, L, h, 128]
+    ring = _ring(1, h, lk, slots=1, batch=2)
+    _k().kv_requant(k.to(DEV), v.to(DEV), ring, 0)
+    q8, qs, _ = _k().quant_q(q.to(DEV))
+    out = _attn_gpu(q, k, v)
+    torch.cuda.synchronize()
+    for b in range(2):
+        rows = slice(b * h, (b + 1) * h)
+        _check_chunk(ring, 0, 0, emu.requant(k[b:b + 1], v[b:b + 1]), lk, bh_slice=rows)
+        r8, rs = emu.quant_q(q[b:b + 1])
+        assert torch.equal(q8.cpu()[rows], r8)
+        torch.testing.assert_close(qs.cpu()[rows], rs, rtol=0, atol=0)
+        qb, kb, vb = q[b:b + 1], k[b:b + 1], v[b:b + 1]
+        ref = emu.attention(qb, [emu.requant(kb, vb)], schedule_gx=_gx())[None]
+        sd = emu.sdpa_fp32(qb, kb, vb)[None]
+        err_emu, err_sdpa, err_scheme = (out[b:b + 1] - ref).abs(), (out[b:b + 1] - sd).abs(), (ref - sd).abs()
+        print(f"batch {b}: vs-emu mean {err_emu.mean():.3e} | vs-sdpa max {err_sdpa.max():.3e} "
+              f"mean {err_sdpa.mean():.3e} | emu vs-sdpa mean {err_scheme.mean():.3e}")
+        # the oracle splits batch 1's tiles into pieces; with 2 x the tiles the kernel's split points differ,
+        # which moves the result only by the merge's rounding
+        assert err_emu.mean() <= 0.1 * err_scheme.mean() + 2e-3 * sd.abs().mean()
+        assert err_sdpa.max() <= 2 * err_scheme.max() + 1e-3
+        assert err_sdpa.mean() <= 1.1 * err_scheme.mean() + 1e-5
+
+
 def test_attention_cfg1_tolerance():
     """cfg 1: one latent frame, [1, 1508, 12, 128], seed 0."""
     q, k, v, _ = emu.make_inputs(1508, 1508)
