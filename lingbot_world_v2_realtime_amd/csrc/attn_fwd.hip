@@ -172,12 +172,24 @@ __device__ __forceinline__ void wait_vm(int n) {
   }
 }
 
+// Global -> LDS loads (M0 = the wave's LDS destination; lane i writes M0 + i * size). Written as inline asm on
+// purpose: the compiler models the builtin as a FLAT access that may touch LDS, and while one may be pending
+// it cannot count LDS reads individually, so every LDS wait in the block loop became lgkmcnt(0), draining all
+// fragment reads in flight before each MFMA pair. Hidden from the compiler, the DMA is waited for only by the
+// explicit vmcnt waits below (in-order retirement keeps the compiler's own vmcnt waits correct, at worst
+// stricter). The s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
 __device__ __forceinline__ void dma16(const void* src, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds_addr(lds)) : "memory", "m0");
 }
 
 __device__ __forceinline__ void dma4(const void* src, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+               :: "v"(src), "s"(lds_addr(lds)) : "memory", "m0");
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
