@@ -225,7 +225,7 @@ XCDS = 8
 
 
 def attn_schedule(n_tiles, nb, gx):
-    """Key-block pieces of every 128-query tile under the kernel's schedule: tiles (head-major) split into 8
+    """Key-block pieces of every Q_TILE-query tile under the kernel's schedule: tiles (head-major) split into 8
     contiguous per-XCD ranges; within a range whole tiles go round-robin to its `gx` workgroups while each
     gets one, and the rest's (tile, block) units are cut into `gx` equal contiguous pieces.
     Returns {tile: [(j0, j1), ...]} with pieces in increasing j0 (the merge order)."""

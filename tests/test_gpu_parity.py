@@ -250,6 +250,50 @@ def test_memory_ring_attention():
     assert e_sd.max() <= 2 * e_scheme.max()
 
 
+def test_memory_ring_ragged_chunks():
+    """Chunks of different lengths (a full 700-key chunk, 333, 65, and a 129-key current chunk) and a custom
+    sm_scale: masked key tails inside the chunk sequence, chunk switches inside split pieces."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    h, cl, lq, sm = 3, 700, 300, 0.06
+    g = torch.Generator().manual_seed(77)
+    ks, vs = [], []
+    for n in (700, 333, 65, 129):
+        ks.append((torch.randn(1, n, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16())
+        vs.append(torch.randn(1, n, h, 128, generator=g).bfloat16())
+    q = torch.randn(1, lq, h, 128, generator=g).bfloat16()
+    ring = QuantKVRing(1, 1, h, cl, slots=4, device=DEV)
+    for kk, vv in zip(ks[:-1], vs[:-1]):
+        ring.write(0, kk.to(DEV), vv.to(DEV))
+        ring.commit()
+    ring.write(0, ks[-1].to(DEV), vs[-1].to(DEV))
+    out = ring.attend(q.to(DEV), 0, sm_scale=sm).float().cpu()
+    ref = emu.attention(q, [emu.requant(kk, vv) for kk, vv in zip(ks, vs)], sm_scale=sm, schedule_gx=_gx())[None]
+    sd = emu.sdpa_fp32(q, torch.cat(ks, 1), torch.cat(vs, 1), sm_scale=sm)[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    print(f"ragged ring vs-emu mean {e_emu.mean():.3e}; vs-sdpa max {e_sd.max():.3e} mean {e_sd.mean():.3e}; "
+          f"emu vs-sdpa max {e_scheme.max():.3e} mean {e_scheme.mean():.3e}")
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
+    assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
+
+
+def test_hnd_layout_same_bits():
+    """tensor_layout="HND" ([B, H, L, 128]) reads the same elements through other strides: the output is the
+    NHD call's, bit for bit, with a custom sm_scale, and it is close to fp32 SDPA."""
+    from lingbot_world_v2_realtime_amd import sage_attention
+    q, k, v, _ = emu.make_inputs(333, 517, h=5, seed=9)
+    qd, kd, vd = (x.to(DEV) for x in (q, k, v))
+    nhd = sage_attention(qd, kd, vd, sm_scale=0.07)
+    hnd = sage_attention(*(x.transpose(1, 2).contiguous() for x in (qd, kd, vd)), tensor_layout="HND",
+                         sm_scale=0.07)
+    assert hnd.shape == (1, 5, 333, 128)
+    assert torch.equal(hnd.transpose(1, 2).cpu(), nhd.cpu())
+    sd = emu.sdpa_fp32(q, k, v, sm_scale=0.07)[None]
+    err = (nhd.float().cpu() - sd).abs()
+    print(f"hnd/nhd vs-sdpa max {err.max():.3e} mean {err.mean():.3e}")
+    assert err.max() < 2e-2 and err.mean() < 2e-3
+
+
 def _sdpa_gpu_fp32(q, k, v):
     """fp32 softmax attention on the GPU, per head: [1, L, H, D] bf16 -> fp32 [1, Lq, H, D]."""
     qd, kd, vd = (x.to(DEV).float() for x in (q, k, v))
