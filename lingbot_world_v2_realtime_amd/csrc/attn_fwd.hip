@@ -16,6 +16,8 @@
 // gets one; the remaining tiles' (tile, key block) units are cut into equal contiguous pieces, one per
 // workgroup. A piece that is not a whole tile leaves an unnormalised partial (O, running max, row sum) in the
 // workspace, and attn_merge_kernel combines the pieces of each split tile.
+#include <atomic>
+
 #include "lbw_common.h"
 
 namespace lbw {
@@ -696,17 +698,20 @@ __global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict
     for (int i = 0; i < 16; ++i) op[32 * mt + 8 * (i >> 2) + 4 * g + (i & 3)] = acc[mt][i];
 }
 
-// Persistent workgroups per XCD: one per CU (a workgroup is 8 waves, two per SIMD, and uses 120 KB of LDS).
+// Persistent workgroups per XCD: one per CU (a workgroup is 8 waves, two per SIMD, and uses AT_LDS bytes of the
+// CU's 160 KB of LDS). Cached per device ordinal; atomic, since entry points may run on several host threads.
 static int attn_wgs_per_xcd() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];   // 0 unknown (static storage: zero-initialised)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
-  if (cached[dev] == 0) {
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    cached[dev] = (cus + XCDS - 1) / XCDS;
+    v = (cus + XCDS - 1) / XCDS;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return v;
 }
 
 }  // namespace lbw

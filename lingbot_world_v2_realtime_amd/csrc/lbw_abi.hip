@@ -1,4 +1,5 @@
 // Status strings and version of the C-ABI.
+#include <atomic>
 #include <cstring>
 
 #include "lbw_common.h"
@@ -21,17 +22,20 @@ extern "C" int lbw_version(void) { return 100; }
 namespace lbw {
 
 // LBW_OK when the current device is a gfx950 (the only target the code objects are built for), else
-// LBW_E_DEVICE; the answer is cached per device ordinal.
+// LBW_E_DEVICE; the answer is cached per device ordinal. Entry points may run on several host threads at once:
+// the cache is atomic (every thread that misses computes and stores the same value).
 int check_device() {
-  static int cached[64] = {0};   // 0 unknown, 1 gfx950, 2 other
+  static std::atomic<int> cached[64];   // 0 unknown, 1 gfx950, 2 other (static storage: zero-initialised)
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return LBW_E_DEVICE;
-  if (cached[dev] == 0) {
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return LBW_E_DEVICE;
-    cached[dev] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+    v = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev] == 1 ? LBW_OK : LBW_E_DEVICE;
+  return v == 1 ? LBW_OK : LBW_E_DEVICE;
 }
 
 }  // namespace lbw

@@ -145,7 +145,13 @@ def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_le
     n_seg = len(seg_slots)
     if not 1 <= n_seg <= MAX_SEGMENTS or len(seg_lens) != n_seg:
         raise ValueError(f"need 1..{MAX_SEGMENTS} chunks with a length each, got {seg_slots} / {seg_lens}")
-    _, _, _, o_b, o_t, o_h = _dims(out, layout)
+    _require_cuda_bf16("out", out)
+    ob, ol, oh, o_b, o_t, o_h = _dims(out, layout)
+    if (ob, ol, oh) != (batch, lq, heads):   # the kernel writes every row of this shape through out's strides
+        raise ValueError(f"out {tuple(out.shape)} ({layout}) does not hold batch {batch} x {lq} rows x {heads} heads")
+    if q8.shape[0] != batch * heads or q8.shape[1] < lq or q_scale.shape[0] != batch * heads:
+        raise ValueError(f"q8 {tuple(q8.shape)} / q_scale {tuple(q_scale.shape)} do not match batch {batch}, "
+                         f"heads {heads}, lq {lq}")
     sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
     k8, ksc, _, v8, v8lo, vsc = ring.layer_view(layer)
     slot_arr = (ctypes_i32 * n_seg)(*seg_slots)

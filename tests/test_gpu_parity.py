@@ -384,3 +384,24 @@ def test_graph_replay_matches_eager():
         assert torch.equal(ring.cache.k8[:, ring.current], k8_eager[:, ring.current])
         chunk()   # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_attn_fwd_refuses_mismatched_buffers():
+    """The wrapper checks out / q8 against (batch, lq, heads) before launching: a smaller out would be written
+    past its end through its own strides."""
+    from lingbot_world_v2_realtime_amd import kernels
+    q, k, v, _ = emu.make_inputs(100, 130, h=2, seed=3)
+    ring = _ring(1, 2, 130, slots=1)
+    kernels.kv_requant(k.to(DEV), v.to(DEV), ring, 0)
+    q8, qs, _ = kernels.quant_q(q.to(DEV))
+    good = torch.empty(1, 100, 2, 128, dtype=torch.bfloat16, device=DEV)
+    kernels.attn_fwd(q8, qs, None, 1, 100, 2, ring, 0, [0], [130], good)
+    for bad in (torch.empty(1, 99, 2, 128, dtype=torch.bfloat16, device=DEV),
+                torch.empty(1, 100, 1, 128, dtype=torch.bfloat16, device=DEV),
+                torch.empty(1, 100, 2, 128, dtype=torch.float32, device=DEV)):
+        with pytest.raises((ValueError, TypeError)):
+            kernels.attn_fwd(q8, qs, None, 1, 100, 2, ring, 0, [0], [130], bad)
+    with pytest.raises(ValueError):   # q8 holds 256 padded rows: 300 queries do not fit
+        kernels.attn_fwd(q8, qs, None, 1, 300, 2, ring, 0, [0], [130],
+                         torch.empty(1, 300, 2, 128, dtype=torch.bfloat16, device=DEV))
+    torch.cuda.synchronize()
