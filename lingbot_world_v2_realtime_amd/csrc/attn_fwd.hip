@@ -386,16 +386,22 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       vq[1] = vfrag(1);
     }
     __builtin_amdgcn_sched_barrier(0);
-    // DMA of block it + LEAD into the stage of block it - 2 (both groups finished it a phase ago); issued here,
-    // where the wave mostly waits for its LDS reads and the matrix core, instead of in the softmax phase
+    if (do_qk) {
+      acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0], qf[0], magic, 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1], qf[0], magic, 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // DMA of block it + LEAD into the stage of block it - 2 (both groups finished it a phase ago): in the MFMA
+    // phase, where the wave mostly waits for the matrix core (the softmax phase slows down with it), and after
+    // the first two QK MFMAs, so the matrix core starts at once and the issue hides under their execution
+    // (-1 to -2 % against issuing it before them, same-box A/B)
     if (it + LEAD < n) {
       issue(ldstage);
       advance();
       ldstage = ldstage + 1 == NSTAGE ? 0 : ldstage + 1;
     }
+    __builtin_amdgcn_sched_barrier(0);
     if (do_qk) {
-      acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0], qf[0], magic, 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1], qf[0], magic, 0, 0, 0);
 #pragma unroll
       for (int kk = 1; kk < 4; ++kk) {
         acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[2 * kk], qf[kk], acc[0], 0, 0, 0);
