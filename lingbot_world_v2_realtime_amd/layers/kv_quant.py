@@ -10,6 +10,11 @@ per-chunk V scale as a rescale of the accumulator between chunks).
 Slot bookkeeping is host integers only (as lingbot/layers/kv_cache.py:1-6 keeps its window positions), so a
 forward can be captured in a HIP graph. With `slots` = 4 the attended keys are the current chunk plus the
 three most recent saved chunks (a slot-granular version of model_fast_kv_ring.py:28-48's ring).
+
+The reference's window is a sink of the first tokens plus the most recent ones (kv_cache.py:23-58: eviction
+shifts the non-sink part left, the sink stays). `sink_chunks` maps that onto whole chunks: the first
+`sink_chunks` chunks committed keep their slots for good, and a full ring evicts its oldest non-sink chunk.
+`--sink_size 6` frames of 4-frame chunks is 1.5 chunks: sink_chunks=1 keeps the first chunk, 2 a superset.
 """
 from .. import kernels
 
@@ -19,15 +24,19 @@ __all__ = ["QuantKVRing", "alloc_cache", "save_chunk", "attend"]
 class QuantKVRing:
     """Quantised K/V ring of `slots` chunk slots for each of `num_layers` layers."""
 
-    def __init__(self, num_layers, batch, heads, chunk_len, slots=4, device="cuda", v_terms=2):
+    def __init__(self, num_layers, batch, heads, chunk_len, slots=4, device="cuda", v_terms=2, sink_chunks=0):
         if slots < 2 or slots > kernels.MAX_SEGMENTS:
             raise ValueError(f"slots must be in 2..{kernels.MAX_SEGMENTS}")
+        if not 0 <= sink_chunks <= slots - 2:   # at least one rolling slot besides the current one
+            raise ValueError(f"sink_chunks must be in 0..slots - 2 = {slots - 2}")
         self.cache = kernels.RingCache(num_layers, batch, heads, kernels.pad_to(chunk_len, kernels.K_BLOCK),
                                        slots, device, v_terms)
         self.chunk_len = chunk_len
         self.slots = slots
         self.lens = [0] * slots      # valid tokens in each slot (the same for every layer)
-        self.memory = []             # slots holding saved chunks, oldest first
+        self.sink_chunks = sink_chunks
+        self.sink = []               # slots holding the first sink_chunks saved chunks (never evicted)
+        self.memory = []             # slots holding the other saved chunks, oldest first
         self.current = 0             # slot this chunk's K/V are quantised into
         self._ws = {}
 
@@ -53,8 +62,9 @@ class QuantKVRing:
         self.lens[self.current] = n
 
     def attended(self):
-        """(slots, lengths) the attention reads: saved chunks oldest first, then the current chunk."""
-        slots = self.memory + [self.current]
+        """(slots, lengths) the attention reads: the sink chunks, the other saved chunks oldest first, then the
+        current chunk."""
+        slots = self.sink + self.memory + [self.current]
         return slots, [self.lens[s] for s in slots]
 
     def attend(self, q, layer, sm_scale=None):
@@ -68,22 +78,23 @@ class QuantKVRing:
         return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale)
 
     def commit(self):
-        """The chunk is finished (its clean forward was written): it joins the memory. When the memory is
-        full the oldest chunk is evicted and its slot takes the next chunk."""
+        """The chunk is finished (its clean forward was written): it joins the sink while the sink is not full,
+        else the memory. When every slot is taken the oldest non-sink chunk is evicted and its slot takes the
+        next chunk."""
         if self.lens[self.current] == 0:
             raise RuntimeError("nothing written to the current slot")
-        self.memory.append(self.current)
-        if len(self.memory) == self.slots:
+        (self.sink if len(self.sink) < self.sink_chunks else self.memory).append(self.current)
+        if len(self.sink) + len(self.memory) == self.slots:
             self.current = self.memory.pop(0)
         else:
-            used = set(self.memory)
+            used = set(self.sink) | set(self.memory)
             self.current = next(s for s in range(self.slots) if s not in used)
         self.lens[self.current] = 0
 
 
-def alloc_cache(num_layers, batch, heads, chunk_len, slots=4, device="cuda", v_terms=2):
+def alloc_cache(num_layers, batch, heads, chunk_len, slots=4, device="cuda", v_terms=2, sink_chunks=0):
     """A quantised chunk ring (cf. sage_kvq.alloc_cache, experiments/modules/sage_kvq.py:38-48)."""
-    return QuantKVRing(num_layers, batch, heads, chunk_len, slots, device, v_terms)
+    return QuantKVRing(num_layers, batch, heads, chunk_len, slots, device, v_terms, sink_chunks)
 
 
 def save_chunk(ring, layer, k, v):

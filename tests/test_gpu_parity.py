@@ -405,3 +405,29 @@ def test_attn_fwd_refuses_mismatched_buffers():
         kernels.attn_fwd(q8, qs, None, 1, 300, 2, ring, 0, [0], [130],
                          torch.empty(1, 300, 2, 128, dtype=torch.bfloat16, device=DEV))
     torch.cuda.synchronize()
+
+
+def test_ring_with_sink_chunk():
+    """sink_chunks=1, 4 slots, 6 chunks: the attention reads chunk 0 (the sink), chunks 3 and 4 and the current
+    chunk 5, each with its own mean and V scale, and matches the oracle over exactly those chunks."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    h, n = 2, 200
+    g = torch.Generator().manual_seed(55)
+    chunks = [((torch.randn(1, n, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16(),
+               (torch.randn(1, n, h, 128, generator=g) * (1 + 0.3 * i)).bfloat16()) for i in range(6)]
+    q = torch.randn(1, 150, h, 128, generator=g).bfloat16()
+    ring = QuantKVRing(1, 1, h, n, slots=4, device=DEV, sink_chunks=1)
+    for i, (kk, vv) in enumerate(chunks):
+        ring.write(0, kk.to(DEV), vv.to(DEV))
+        if i < 5:
+            ring.commit()
+    assert ring.attended()[0][0] == 0
+    out = ring.attend(q.to(DEV), 0).float().cpu()
+    used = [chunks[i] for i in (0, 3, 4, 5)]
+    ref = emu.attention(q, [emu.requant(kk, vv) for kk, vv in used], schedule_gx=_gx())[None]
+    sd = emu.sdpa_fp32(q, torch.cat([c[0] for c in used], 1), torch.cat([c[1] for c in used], 1))[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    print(f"sink ring vs-emu mean {e_emu.mean():.3e}; vs-sdpa max {e_sd.max():.3e} mean {e_sd.mean():.3e}; "
+          f"emu vs-sdpa mean {e_scheme.mean():.3e}")
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5

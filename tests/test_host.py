@@ -45,6 +45,31 @@ def test_ring_slot_rotation():
         ring.commit()                                # nothing written to the new current slot
 
 
+def test_ring_sink_chunks_stay():
+    """sink_chunks=1 (the reference's sink of first frames, kv_cache.py:23-58, at chunk granularity): the first
+    chunk keeps its slot for good; a full ring evicts the oldest of the others."""
+    ring = kv_quant.QuantKVRing(1, 1, 1, 64, slots=4, device="cpu", sink_chunks=1)
+    seen = []
+    for chunk in range(8):
+        ring.lens[ring.current] = 64 - chunk
+        seen.append(ring.attended())
+        ring.commit()
+    assert seen[0][0] == [0]
+    assert seen[3][0] == [0, 1, 2, 3]
+    assert seen[4][0] == [0, 2, 3, 1]                # chunk 4 takes chunk 1's slot, chunk 0 stays first
+    assert seen[5][0] == [0, 3, 1, 2]
+    assert seen[7][0] == [0, 2, 3, 1]
+    assert seen[7][1] == [64, 59, 58, 57]            # chunk 0's length, then chunks 5, 6 and the current 7
+    two = kv_quant.QuantKVRing(1, 1, 1, 64, slots=4, device="cpu", sink_chunks=2)
+    for chunk in range(6):
+        two.lens[two.current] = 1
+        two.commit()
+    assert two.attended()[0][:2] == [0, 1]
+    for bad in (-1, 3):
+        with pytest.raises(ValueError):
+            kv_quant.QuantKVRing(1, 1, 1, 64, slots=4, device="cpu", sink_chunks=bad)
+
+
 def test_ring_refuses_attend_before_write_and_bad_slots():
     ring = kv_quant.QuantKVRing(1, 1, 1, 64, slots=2, device="cpu")
     with pytest.raises(RuntimeError):
