@@ -633,27 +633,48 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   // workgroups of this XCD whose unit range meets [ua, ub): owner(u) = floor(((u + 1) gx - 1) / units)
   const int i_a = (int)(((ua + 1) * a.gx - 1) / p.units);
   const int i_b = (int)((ub * a.gx - 1) / p.units);
-  const int64_t i_a_u0 = (int64_t)i_a * p.units / a.gx, i_a_u1 = (int64_t)(i_a + 1) * p.units / a.gx;
-  if (i_a == i_b && i_a_u0 <= ua && i_a_u1 >= ub) return;   // written whole by one workgroup
+  // workgroup i's units are [floor(i units / gx), floor((i + 1) units / gx)): stepped from i_a with the quotient
+  // and remainder of units / gx, so the loops below divide nothing (64-bit divisions are long instruction
+  // sequences, and this kernel is short)
+  const int64_t uq = p.units / a.gx;
+  const int ur = (int)(p.units % a.gx);
+  const int64_t lo_a = (int64_t)i_a * uq + (int64_t)i_a * ur / a.gx;
+  const int rem_a = (int)((int64_t)i_a * ur % a.gx);
+  const int64_t hi_a = lo_a + uq + (rem_a + ur >= a.gx ? 1 : 0);
+  if (i_a == i_b && lo_a <= ua && hi_a >= ub) return;   // written whole by one workgroup
   const int t = threadIdx.x, row = slab * MERGE_ROWS + (t >> 4), c0 = (t & 15) * 8;
   const int64_t q = (int64_t)(tile % a.q_tiles) * QT + row;
   if (q >= a.lq) return;
+  // a piece of workgroup ii that meets this tile is in its partial slot 0 when the tile is the first of
+  // the workgroup's range, i.e. when the piece starts inside the tile, else in slot 1
   float mmax = -INFINITY;
-  for (int ii = i_a; ii <= i_b; ++ii) {
-    const int64_t w0 = (int64_t)ii * p.units / a.gx, w1 = (int64_t)(ii + 1) * p.units / a.gx;
-    if (w0 == w1 || w1 <= ua || w0 >= ub) continue;   // no units of this tile
-    const int ft = p.ts + (int)(w0 / a.nb);
-    const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (tile == ft ? 0 : 1);
-    mmax = fmaxf(mmax, ml_part[(slot * QT + row) * 2]);
+  {
+    int64_t lo = lo_a;
+    int rem = rem_a;
+    for (int ii = i_a; ii <= i_b; ++ii) {
+      const bool carry = rem + ur >= a.gx;
+      const int64_t hi = lo + uq + (carry ? 1 : 0);
+      rem += ur - (carry ? a.gx : 0);
+      if (hi > lo && hi > ua && lo < ub) {   // units of this tile
+        const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (lo >= ua ? 0 : 1);
+        mmax = fmaxf(mmax, ml_part[(slot * QT + row) * 2]);
+      }
+      lo = hi;
+    }
   }
   float acc[8], den = 0.f;
 #pragma unroll
   for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+  int64_t lo = lo_a;
+  int rem = rem_a;
   for (int ii = i_a; ii <= i_b; ++ii) {
-    const int64_t w0 = (int64_t)ii * p.units / a.gx, w1 = (int64_t)(ii + 1) * p.units / a.gx;
-    if (w0 == w1 || w1 <= ua || w0 >= ub) continue;
-    const int ft = p.ts + (int)(w0 / a.nb);
-    const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (tile == ft ? 0 : 1);
+    const bool carry = rem + ur >= a.gx;
+    const int64_t hi = lo + uq + (carry ? 1 : 0);
+    rem += ur - (carry ? a.gx : 0);
+    const int64_t plo = lo;
+    lo = hi;
+    if (!(hi > plo && hi > ua && plo < ub)) continue;
+    const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (plo >= ua ? 0 : 1);
     const float2 ml = *(const float2*)(ml_part + (slot * QT + row) * 2);
     const float wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
     den += wgt * ml.y;
