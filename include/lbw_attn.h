@@ -115,7 +115,7 @@ int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias,
  * is split between workgroups); independent of the problem size. */
 int64_t lbw_attn_workspace_bytes(void);
 
-/* Persistent workgroups per XCD that lbw_attn_fwd launches on the current device (two per CU). Query tiles
+/* Persistent workgroups per XCD that lbw_attn_fwd launches on the current device (one per CU). Query tiles
  * are dealt to XCDs in 8 contiguous ranges and, within one, whole tiles go round-robin to these workgroups
  * while each gets one; the remaining tiles' key blocks are cut into equal contiguous pieces, one per
  * workgroup. Exposed so a checker can reproduce the pieces (each piece rounds P against its own running max). */
