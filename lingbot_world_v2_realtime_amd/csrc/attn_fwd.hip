@@ -179,19 +179,24 @@ __device__ __forceinline__ void wait_vm(int n) {
 // it cannot count LDS reads individually, so every LDS wait in the block loop became lgkmcnt(0), draining all
 // fragment reads in flight before each MFMA pair. Hidden from the compiler, the DMA is waited for only by the
 // explicit vmcnt waits below (in-order retirement keeps the compiler's own vmcnt waits correct, at worst
-// stricter). The s_nop covers the M0-write -> LDS-DMA hazard.
+// stricter). The s_nop covers the M0-write -> LDS-DMA hazard. M0 is a reserved register the compiler does not
+// let inline asm clobber, so the asm saves and restores it.
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
 
 __device__ __forceinline__ void dma16(const void* src, uint8_t* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(src), "s"(lds_addr(lds)) : "memory");
 }
 
 __device__ __forceinline__ void dma4(const void* src, uint8_t* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-               :: "v"(src), "s"(lds_addr(lds)) : "memory", "m0");
+  uint32_t keep;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(src), "s"(lds_addr(lds)) : "memory");
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
