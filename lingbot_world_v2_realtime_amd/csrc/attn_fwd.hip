@@ -53,18 +53,13 @@ __device__ __forceinline__ XcdPlan xcd_plan(const AttnArgs& a, int x) {
   return p;
 }
 
-// LDS stage: K tile of 64 rows x 128 bytes with rows padded to 144 bytes, then the V block of 128 rows
-// (channels) x 64 bytes with rows padded to 80 bytes. Row strides of 9 and 5 sixteen-byte units are odd, so the
-// 16 lanes an LDS b128 access serves at a time (16 consecutive rows, same chunk) hit 16 distinct bank groups,
-// and every fragment address is a per-lane base plus a compile-time offset.
-constexpr int K_ROW = 144, V_ROW = 80;
+// K tile of the debug logits kernel in LDS: 64 rows x 128 bytes with rows padded to 144 bytes. The row stride
+// of 9 sixteen-byte units is odd, so the 16 lanes an LDS b128 access serves at a time (16 consecutive rows,
+// same chunk) hit 16 distinct bank groups. (The attention's stages XOR-swizzle their chunks instead.)
+constexpr int K_ROW = 144;
 constexpr int K_LDS = KB * K_ROW;              // 9216
-constexpr int V_LDS = D * V_ROW;               // 10240
-constexpr int STAGE_BYTES = K_LDS + 2 * V_LDS; // 29696: K, V (hi plane), V (lo plane, when present)
 constexpr int S_MASKED = (int)0xFF800000;      // bits of -inf: the int max ignores it, exp2 gives 0
 __device__ __forceinline__ int k_lds_off(int row, int ch) { return row * K_ROW + (ch << 4); }
-__device__ __forceinline__ int v_lds_off(int row, int ch) { return K_LDS + row * V_ROW + (ch << 4); }
-constexpr int VLO_LDS_OFF = V_LDS;             // the lo plane follows the hi plane: v_lds_off(..) + VLO_LDS_OFF
 constexpr int E8M0_ONE = 0x7F7F7F7F;           // MFMA block scale 1.0 in every byte
 constexpr int E8M0_LO = 0x7B7B7B7B;            // 2^-4: the lo plane carries (y - hi) * 16
 
@@ -286,10 +281,9 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     }
   };
 
-  // compute cursor: chunk c and chunk-relative block blk of the block in the softmax
+  // compute cursor: chunk c of the block in the softmax and the blocks it has left
   int c = 0;
   while (j0 >= a.seg_blk0[c + 1]) ++c;
-  int blk = j0 - a.seg_blk0[c];
   int crem = a.seg_blk0[c + 1] - j0;                   // blocks left in chunk c, this one included
   int last_valid = a.seg_len[c] - (a.seg_blk0[c + 1] - a.seg_blk0[c] - 1) * KB;   // keys in its last block
   int c_prev = c;
@@ -447,7 +441,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     }
     phase_barrier();
 
-    // ---- softmax phase for block it (chunk c, block blk) ----
+    // ---- softmax phase for block it (chunk c) ----
     if (c != c_prev) {
       // a new chunk (c_prev == c - 1: every chunk has a block): O (blocks before this one) to its V scale,
       // and its logit bias, both from the piece's LDS tables
@@ -507,11 +501,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     // next block of the compute cursor
     if (--crem == 0 && c + 1 < a.n_seg) {
       ++c;
-      blk = 0;
       crem = a.seg_blk0[c + 1] - a.seg_blk0[c];
       last_valid = a.seg_len[c] - (crem - 1) * KB;
-    } else {
-      ++blk;
     }
     if (grp_a) {   // A's pieces of block it + 1 have landed (blocks up to it + LEAD may still be in flight)
       if (it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
