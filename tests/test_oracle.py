@@ -2,7 +2,6 @@
 written from the format definition, round-half-even ties, closed forms, exact invariances, int64 brute force,
 fp32 softmax attention, and the split-KV merge identity. No GPU needed."""
 import math
-import struct
 
 import numpy as np
 import pytest
