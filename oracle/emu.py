@@ -192,8 +192,9 @@ def requant(k, v):
 
 def dequant_v(chunk, terms=None):
     """e4m3 V of a quantised chunk back to fp32 [H, n, D] in key order, without the V scale: hi + lo / 16
-    (or hi alone with terms=1)."""
-    terms = V_TERMS if terms is None else terms
+    (or hi alone with terms=1, the default for a chunk whose "v8lo" is None)."""
+    if terms is None:   # a chunk quantised without the residual plane has one term
+        terms = V_TERMS if chunk.get("v8lo") is not None else 1
     h, nb, d, _ = chunk["v8"].shape
     out = 0
     for bits, w in ((chunk["v8"], 1.0), (chunk["v8lo"], 1.0 / V_LO_SCALE))[:terms]:

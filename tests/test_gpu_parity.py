@@ -431,3 +431,31 @@ def test_ring_with_sink_chunk():
           f"emu vs-sdpa mean {e_scheme.mean():.3e}")
     assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
     assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
+
+
+def test_one_plane_path():
+    """A ring without the residual V plane (v_terms=1): the re-quant writes the e4m3 plane bit-exact and no
+    second one, and the attention kernel built for one plane matches the oracle with one V term over two chunks."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    h, n = 3, 500
+    q, k, v, mem = emu.make_inputs(300, n, h=h, seed=21, mem_chunks=1, chunk_len=n)
+    ring = QuantKVRing(1, 1, h, n, slots=2, device=DEV, v_terms=1)
+    assert ring.cache.v8lo is None
+    ring.write(0, mem[0][0].to(DEV), mem[0][1].to(DEV))
+    ring.commit()
+    ring.write(0, k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    refs = []
+    for slot, (kk, vv) in zip(ring.attended()[0], [mem[0], (k, v)]):
+        r = emu.requant(kk, vv)
+        r["v8lo"] = None
+        _check_chunk(ring.cache, 0, slot, r, n)
+        refs.append(r)
+    out = ring.attend(q.to(DEV), 0).float().cpu()
+    ref = emu.attention(q, refs, schedule_gx=_gx())[None]
+    sd = emu.sdpa_fp32(q, torch.cat([mem[0][0], k], 1), torch.cat([mem[0][1], v], 1))[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    print(f"one plane vs-emu mean {e_emu.mean():.3e}; vs-sdpa mean {e_sd.mean():.3e}; emu vs-sdpa mean "
+          f"{e_scheme.mean():.3e}")
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
