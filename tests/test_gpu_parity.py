@@ -168,6 +168,23 @@ def test_attention_small_vs_oracle(lq, lk):
     assert err_sdpa.mean() <= 1.1 * err_scheme.mean() + 1e-5
 
 
+def test_split_tiles_every_piece():
+    """36 query tiles (6 heads x 1508 queries) over 8 XCDs: each XCD has fewer tiles than workgroups, so every
+    tile's 24 key blocks are cut into pieces of several workgroups (at 32 workgroups per XCD, pieces of 1-4
+    blocks) and merged from the partials. Two calls give the same bits and match the oracle's schedule."""
+    gx = _gx()
+    assert 36 // 8 + 1 < gx                          # no XCD gets a whole-tile round
+    q, k, v, _ = emu.make_inputs(1508, 1508, h=6, seed=77)
+    outs = [_attn_gpu(q, k, v) for _ in range(2)]
+    assert torch.equal(outs[0], outs[1])
+    ref = emu.attention(q, [emu.requant(k, v)], schedule_gx=gx)[None]
+    sd = emu.sdpa_fp32(q, k, v)[None]
+    err_emu, err_scheme = (outs[0] - ref).abs(), (ref - sd).abs()
+    print(f"split tiles vs-emu max {err_emu.max():.3e} mean {err_emu.mean():.3e}; "
+          f"emu vs-sdpa mean {err_scheme.mean():.3e}")
+    assert err_emu.mean() <= 0.1 * err_scheme.mean() + 2e-3 * sd.abs().mean()
+
+
 def test_batch_two():
     """Batch 2 (batch * heads rows of every buffer): each batch element's int8 K / V / Q, scales and means are
     the oracle's for that element alone, bit for bit, and its attention output is as close to the oracle and
