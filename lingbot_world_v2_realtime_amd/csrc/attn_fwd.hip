@@ -643,18 +643,21 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   if (q >= a.lq) return;
   // a piece of workgroup ii that meets this tile is in its partial slot 0 when the tile is the first of
   // the workgroup's range, i.e. when the piece starts inside the tile, else in slot 1
+  // The loads do not depend on whether workgroup ii's range meets the tile (every slot index stays inside the
+  // workspace, ii < gx), so they are issued unconditionally and unrolled to keep several in flight; a slot of a
+  // workgroup with no units here is read but not used (select, not multiply: it may hold anything).
   float mmax = -INFINITY;
   {
     int64_t lo = lo_a;
     int rem = rem_a;
+#pragma unroll 4
     for (int ii = i_a; ii <= i_b; ++ii) {
       const bool carry = rem + ur >= a.gx;
       const int64_t hi = lo + uq + (carry ? 1 : 0);
       rem += ur - (carry ? a.gx : 0);
-      if (hi > lo && hi > ua && lo < ub) {   // units of this tile
-        const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (lo >= ua ? 0 : 1);
-        mmax = fmaxf(mmax, ml_part[(slot * QT + row) * 2]);
-      }
+      const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (lo >= ua ? 0 : 1);
+      const float m = ml_part[(slot * QT + row) * 2];
+      if (hi > lo && hi > ua && lo < ub) mmax = fmaxf(mmax, m);   // units of this tile
       lo = hi;
     }
   }
@@ -663,21 +666,23 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   for (int c = 0; c < 8; ++c) acc[c] = 0.f;
   int64_t lo = lo_a;
   int rem = rem_a;
+#pragma unroll 4
   for (int ii = i_a; ii <= i_b; ++ii) {
     const bool carry = rem + ur >= a.gx;
     const int64_t hi = lo + uq + (carry ? 1 : 0);
     rem += ur - (carry ? a.gx : 0);
     const int64_t plo = lo;
     lo = hi;
-    if (!(hi > plo && hi > ua && plo < ub)) continue;
     const int64_t slot = (int64_t)(ii * XCDS + x) * 2 + (plo >= ua ? 0 : 1);
     const float2 ml = *(const float2*)(ml_part + (slot * QT + row) * 2);
-    const float wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
-    den += wgt * ml.y;
     const float* op = o_part + (slot * QT + row) * D + c0;
     const float4 v0 = *(const float4*)op, v1 = *(const float4*)(op + 4);
-    acc[0] += wgt * v0.x; acc[1] += wgt * v0.y; acc[2] += wgt * v0.z; acc[3] += wgt * v0.w;
-    acc[4] += wgt * v1.x; acc[5] += wgt * v1.y; acc[6] += wgt * v1.z; acc[7] += wgt * v1.w;
+    if (hi > plo && hi > ua && plo < ub) {
+      const float wgt = __builtin_amdgcn_exp2f(ml.x - mmax);
+      den += wgt * ml.y;
+      acc[0] += wgt * v0.x; acc[1] += wgt * v0.y; acc[2] += wgt * v0.z; acc[3] += wgt * v0.w;
+      acc[4] += wgt * v1.x; acc[5] += wgt * v1.y; acc[6] += wgt * v1.z; acc[7] += wgt * v1.w;
+    }
   }
   const float inv = 1.f / den;
   const int bh = tile / a.q_tiles;
