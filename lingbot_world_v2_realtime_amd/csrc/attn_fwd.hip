@@ -650,7 +650,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   {
     int64_t lo = lo_a;
     int rem = rem_a;
-#pragma unroll 4
+#pragma unroll 8
     for (int ii = i_a; ii <= i_b; ++ii) {
       const bool carry = rem + ur >= a.gx;
       const int64_t hi = lo + uq + (carry ? 1 : 0);
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   for (int c = 0; c < 8; ++c) acc[c] = 0.f;
   int64_t lo = lo_a;
   int rem = rem_a;
-#pragma unroll 4
+#pragma unroll 8
   for (int ii = i_a; ii <= i_b; ++ii) {
     const bool carry = rem + ur >= a.gx;
     const int64_t hi = lo + uq + (carry ? 1 : 0);
