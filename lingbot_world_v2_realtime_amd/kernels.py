@@ -43,21 +43,26 @@ class RingCache:
     v_scale fp32 [L, S, BH, 128].
     """
 
-    def __init__(self, layers, batch, heads, cap, slots, device, v_terms=2):
+    def __init__(self, layers, batch, heads, cap, slots, device, v_terms=2, zero=True):
         if cap % K_BLOCK:
             raise ValueError("cap must be a multiple of 64")
+        if v_terms not in (1, 2):
+            raise ValueError("v_terms must be 1 or 2")
         self.layers, self.batch, self.heads, self.cap, self.slots = layers, batch, heads, cap, slots
         bh, nb = batch * heads, cap // K_BLOCK
         dev = torch.device(device)
-        self.k8 = torch.zeros(layers, slots, bh, cap, HEAD_DIM, dtype=torch.int8, device=dev)
-        self.k_scale = torch.zeros(layers, slots, bh, nb, dtype=torch.float32, device=dev)
-        self.km = torch.zeros(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
-        if v_terms not in (1, 2):
-            raise ValueError("v_terms must be 1 or 2")
+        # zero=False leaves the memory uninitialised: for a ring whose every attended block is re-quantised before
+        # it is read (the drop-in call re-quantises the whole window), clearing it is wasted bandwidth
+        new = torch.zeros if zero else torch.empty
+        self.k8 = new(layers, slots, bh, cap, HEAD_DIM, dtype=torch.int8, device=dev)
+        self.k_scale = new(layers, slots, bh, nb, dtype=torch.float32, device=dev)
+        self.km = new(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
         self.v_terms = v_terms
-        self.v8 = torch.zeros(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev)
-        self.v8lo = torch.zeros_like(self.v8) if v_terms == 2 else None
-        self.v_scale = torch.ones(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
+        self.v8 = new(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev)
+        self.v8lo = new(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev) \
+            if v_terms == 2 else None
+        self.v_scale = (torch.ones if zero else torch.empty)(layers, slots, bh, HEAD_DIM, dtype=torch.float32,
+                                                             device=dev)
         self.device = dev
 
     @property
@@ -127,13 +132,18 @@ def quant_q(q, layout="NHD", ring=None, layer=0, seg_slots=()):
 _ATTN_WS = {}
 
 
-def attn_workspace(device):
-    """The attention's scratch for `device` (partials of split query tiles), allocated once per device."""
+def attn_workspace(device, stream=None):
+    """The attention's scratch (partials of split query tiles) for `device` and the stream the call is launched
+    on, allocated once per (device, stream): calls on different streams may run at the same time, and calls that
+    share a workspace must not overlap."""
     dev = torch.device(device)
-    key = (dev.type, dev.index if dev.index is not None else torch.cuda.current_device())
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if stream is None:
+        stream = torch.cuda.current_stream(idx).cuda_stream
+    key = (dev.type, idx, stream)
     if key not in _ATTN_WS:
         nbytes = _lib.load().lbw_attn_workspace_bytes()
-        _ATTN_WS[key] = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+        _ATTN_WS[key] = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=torch.device(dev.type, idx))
     return _ATTN_WS[key]
 
 
@@ -149,15 +159,28 @@ def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_le
     ob, ol, oh, o_b, o_t, o_h = _dims(out, layout)
     if (ob, ol, oh) != (batch, lq, heads):   # the kernel writes every row of this shape through out's strides
         raise ValueError(f"out {tuple(out.shape)} ({layout}) does not hold batch {batch} x {lq} rows x {heads} heads")
-    if q8.shape[0] != batch * heads or q8.shape[1] < lq or q_scale.shape[0] != batch * heads:
-        raise ValueError(f"q8 {tuple(q8.shape)} / q_scale {tuple(q_scale.shape)} do not match batch {batch}, "
-                         f"heads {heads}, lq {lq}")
+    bh, lp = batch * heads, pad_to(lq, Q_TILE)
+    # the kernel strides q8, q_scale and bias by the padded row count of *this* lq: buffers quantised for another
+    # length would be read past their end or row-shifted
+    if (q8.dtype != torch.int8 or tuple(q8.shape) != (bh, lp, HEAD_DIM) or not q8.is_contiguous()
+            or q_scale.dtype != torch.float32 or tuple(q_scale.shape) != (bh, lp // Q_GROUP)
+            or not q_scale.is_contiguous()):
+        raise ValueError(f"q8 {tuple(q8.shape)} / q_scale {tuple(q_scale.shape)} must be contiguous int8 "
+                         f"({bh}, {lp}, {HEAD_DIM}) / fp32 ({bh}, {lp // Q_GROUP}) for batch {batch}, heads {heads}, "
+                         f"lq {lq}")
+    if n_seg == 1:
+        if bias is not None:
+            raise ValueError("one chunk needs no logit bias: pass bias=None")
+    elif (bias is None or bias.dtype != torch.float32 or tuple(bias.shape) != (n_seg, bh, lp)
+          or not bias.is_contiguous()):
+        raise ValueError(f"{n_seg} chunks need a contiguous fp32 bias ({n_seg}, {bh}, {lp}), got "
+                         f"{None if bias is None else tuple(bias.shape)}")
     sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
     k8, ksc, _, v8, v8lo, vsc = ring.layer_view(layer)
     slot_arr = (ctypes_i32 * n_seg)(*seg_slots)
     len_arr = (ctypes_i32 * n_seg)(*seg_lens)
     if workspace is None:
-        workspace = attn_workspace(q8.device)
+        workspace = attn_workspace(q8.device, _stream(q8))
     st = lib.lbw_attn_fwd(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
                           _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr, _ptr(out),
                           o_b, o_t, o_h, sm_scale, _ptr(workspace), _stream(q8))

@@ -17,6 +17,22 @@ __all__ = ["attention", "flash_attention", "sage_attention"]
 
 _QUANT = os.environ.get("LINGBOT_ATTN") in ("sage", "sage_kvq")
 
+# Per-call buffers of the drop-in, kept across calls: (batch, heads, padded keys, device, stream) -> (ring, re-quant
+# workspace). Every block the attention reads is re-quantised by the call itself, so the ring is allocated
+# uninitialised and never cleared; keyed by stream, so calls on different streams never share one.
+_DROPIN = {}
+
+
+def _dropin_buffers(b, h, lk, device):
+    cap = kernels.pad_to(lk, kernels.K_BLOCK)
+    dev = torch.device(device)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (b, h, cap, idx, torch.cuda.current_stream(idx).cuda_stream)
+    if key not in _DROPIN:
+        ring = kernels.RingCache(1, b, h, cap, 1, dev, zero=False)
+        _DROPIN[key] = (ring, kernels.requant_workspace(1, b * h, cap, dev))
+    return _DROPIN[key]
+
 
 def sage_attention(q, k, v, tensor_layout="NHD", is_causal=False, sm_scale=None):
     """Quantized attention, the call `sageattn(q, k, v, tensor_layout, is_causal, sm_scale)` makes on sm_120
@@ -36,8 +52,8 @@ def sage_attention(q, k, v, tensor_layout="NHD", is_causal=False, sm_scale=None)
         raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)} do not match")
     if tensor_layout == "HND":
         k, v = k.transpose(1, 2), v.transpose(1, 2)
-    ring = kernels.RingCache(1, b, h, kernels.pad_to(lk, kernels.K_BLOCK), 1, q.device)
-    kernels.kv_requant(k, v, ring, 0)
+    ring, ws = _dropin_buffers(b, h, lk, q.device)
+    kernels.kv_requant(k, v, ring, 0, workspace=ws)
     q8, qs, _ = kernels.quant_q(q, tensor_layout)
     out = torch.empty_like(q)
     return kernels.attn_fwd(q8, qs, None, b, lq, h, ring, 0, [0], [lk], out, tensor_layout, sm_scale)

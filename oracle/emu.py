@@ -247,10 +247,11 @@ def attn_schedule(n_tiles, nb, gx):
     return pieces
 
 
-def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=None):
+def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=None, p_round=True):
     """Online softmax over tile-relative key blocks [j0, j1) (numbered across the chunks in order) for the
     query rows `qf` (q8 as fp32) -> (o in units of the last chunk's V scale, m, l, last chunk index).
-    The reference max m of a row moves only when a block's max exceeds it by more than `tau`."""
+    The reference max m of a row moves only when a block's max exceeds it by more than `tau`. With
+    p_round=False, P enters the PV product unrounded (fp32) instead of as e4m3."""
     rows, d = qf.shape[0], qf.shape[1]
     m_run = torch.full((rows,), float("-inf"))
     l_run = torch.zeros(rows)
@@ -282,13 +283,13 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
             x = (s_int.double() * cb.double()[:, None] + kc[:, None]).float()
             p = torch.exp2(x)
             l_run = l_run + p.sum(dim=1)
-            o = o + torch.matmul(e4m3_decode(e4m3_encode(p)), vdec[ci][hh, k0:k1])
+            o = o + torch.matmul(e4m3_decode(e4m3_encode(p)) if p_round else p, vdec[ci][hh, k0:k1])
         vs_prev, c_last = vs, ci
         j += nbc
     return o, m_run, l_run, c_last
 
 
-def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None, stats=None):
+def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None, stats=None, p_round=True):
     """Emulated quantized attention of q bf16 [Lq, H, D] over quantised chunks (dicts from `requant`), in the
     kernel's own order: chunks in sequence, 64-key blocks in sequence, a reference row max m, and per block
       b = max_j S_ij * cb + beta,  m_new = b if b > m + tau else m,  alpha = exp2(m - m_new),
@@ -297,7 +298,9 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
     with cb = q_scale * k_scale * sm_scale * log2(e); at a chunk boundary o is rescaled by
     v_scale_old / v_scale_new per channel; finally out = o * v_scale / l.
     With `schedule_gx` (the kernel's workgroups per XCD), tiles the kernel splits between workgroups are
-    computed piece by piece from a fresh state and merged as O = sum 2^(m_i - M) o_i / sum 2^(m_i - M) l_i.
+    computed piece by piece from a fresh state and merged by `merge_partials`.
+    p_round=False skips the e4m3 rounding of P (a checking mode: the result is then exact softmax attention of
+    the dequantised logits and V, whatever the block order, running max or split).
     Returns fp32 [Lq, H, D].
     """
     q = _as_lhd(q)
@@ -337,21 +340,14 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
             qsr = qsr_all[hh, a:e]
             beta_of = (lambda ci: bias[ci][hh, a:e]) if multi else (lambda ci: torch.zeros(e - a))
             if t is None:
-                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, 0, nb, sl2, tau, stats)
+                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, 0, nb, sl2, tau, stats, p_round)
                 out[a:e, hh] = (o * chunks[cl]["v_scale"][hh][None, :]) * (1.0 / l)[:, None]
                 continue
             parts = []
             for j0, j1 in sched[hh * q_tiles + t]:
-                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats)
+                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats, p_round)
                 parts.append((o * chunks[cl]["v_scale"][hh][None, :], m, l))
-            mmax = torch.stack([pm for _, pm, _ in parts]).amax(dim=0)
-            num = torch.zeros(e - a, d)
-            den = torch.zeros(e - a)
-            for po, pm, pl in parts:
-                wgt = torch.exp2(pm - mmax)
-                den = den + wgt * pl
-                num = num + wgt[:, None] * po
-            out[a:e, hh] = num * (1.0 / den)[:, None]
+            out[a:e, hh] = merge_partials(parts)
     return out
 
 
@@ -406,12 +402,17 @@ def sdpa_fp32(q, k, v, sm_scale=None):
 def merge_partials(parts):
     """Split-KV merge (experiments/bench_attn/splitkv/README.md:62) in the exp2 domain.
 
-    parts: list of (o_unnormalised [Lq, D], m [Lq], d [Lq]); returns O = sum 2^(m_i - m) o_i / sum 2^(m_i - m) d_i.
-    """
+    parts: list of (o_unnormalised [Lq, D], m [Lq], d [Lq]), in key order; returns
+    O = sum 2^(m_i - M) o_i * (1 / sum 2^(m_i - M) d_i), M = max m_i, summed piece by piece in the given order
+    (the merge kernel's order and its multiply by the reciprocal)."""
     m = torch.stack([p[1] for p in parts]).amax(dim=0)
-    num = sum(torch.exp2(p[1] - m)[:, None] * p[0] for p in parts)
-    den = sum(torch.exp2(p[1] - m) * p[2] for p in parts)
-    return num / den[:, None]
+    num = torch.zeros_like(parts[0][0])
+    den = torch.zeros_like(parts[0][2])
+    for po, pm, pl in parts:
+        wgt = torch.exp2(pm - m)
+        den = den + wgt * pl
+        num = num + wgt[:, None] * po
+    return num * (1.0 / den)[:, None]
 
 
 def make_inputs(lq, lk, h=12, d=HEAD_DIM, seed=0, mem_chunks=0, chunk_len=None):

@@ -3,6 +3,7 @@ scales, the K mean and the int32 logits; within tolerance for the attention outp
 import pytest
 import torch
 
+from conftest import record
 from oracle import emu
 
 pytestmark = pytest.mark.gpu
@@ -223,12 +224,14 @@ def test_attention_cfg1_tolerance():
     sd = emu.sdpa_fp32(q, k, v)[None]
     ref = emu.attention(q, [emu.requant(k, v)], schedule_gx=_gx())[None]
     e_sd, e_emu = (out - sd).abs(), (out - ref).abs()
-    print(f"cfg1 vs-sdpa max {e_sd.max():.3e} mean {e_sd.mean():.3e}; vs-emu max {e_emu.max():.3e} "
-          f"mean {e_emu.mean():.3e}; emu vs sdpa mean {(ref - sd).abs().mean():.3e}")
-    assert e_sd.max() < SDPA_MAX_ABS
-    # mean-abs at 1508 keys sits at the e4m3 P x e4m3 V floor (the oracle itself is at 1.30e-3)
-    assert e_sd.mean() < 1.5e-3
-    assert e_emu.mean() < 5e-4
+    msg = (f"cfg1 [1,1508,12,128] vs fp32 SDPA: max {e_sd.max():.3e} (gate {SDPA_MAX_ABS:g}) mean {e_sd.mean():.3e} "
+           f"(gate {SDPA_MEAN_ABS:g}); vs oracle mean {e_emu.mean():.3e}; oracle vs SDPA mean "
+           f"{(ref - sd).abs().mean():.3e}")
+    record(msg)
+    # with both e4m3 V planes the scheme's own mean-abs error at 1508 keys is ~9.4e-4 (one plane: ~1.3e-3)
+    assert e_sd.max() < SDPA_MAX_ABS, msg
+    assert e_sd.mean() < SDPA_MEAN_ABS, msg
+    assert e_emu.mean() < 5e-4, msg
 
 
 def test_attention_cfg2_tolerance():
@@ -237,8 +240,10 @@ def test_attention_cfg2_tolerance():
     out = _attn_gpu(q, k, v)
     sd = emu.sdpa_fp32(q, k, v)[None]
     e = (out - sd).abs()
-    print(f"cfg2 vs-sdpa max {e.max():.3e} mean {e.mean():.3e}")
-    assert e.max() < SDPA_MAX_ABS and e.mean() < SDPA_MEAN_ABS
+    msg = (f"cfg2 [1,6032,12,128] vs fp32 SDPA: max {e.max():.3e} (gate {SDPA_MAX_ABS:g}) mean {e.mean():.3e} "
+           f"(gate {SDPA_MEAN_ABS:g})")
+    record(msg)
+    assert e.max() < SDPA_MAX_ABS and e.mean() < SDPA_MEAN_ABS, msg
 
 
 def test_memory_ring_attention():
@@ -337,9 +342,11 @@ def test_attention_cfg3_tolerance():
     vv = torch.cat([m[1] for m in mem] + [v], 1)
     sd = _sdpa_gpu_fp32(q, kk, vv)
     e = (out - sd).abs()
-    print(f"cfg3 vs-sdpa max {e.max():.3e} mean {e.mean():.3e} (|out| mean {sd.abs().mean():.3e})")
-    assert e.mean() < SDPA_MEAN_ABS
-    assert e.max() < SDPA_MAX_ABS
+    msg = (f"cfg3 [1,6032,12,128] x 24128 keys vs fp32 SDPA: max {e.max():.3e} (gate {SDPA_MAX_ABS:g}) mean "
+           f"{e.mean():.3e} (gate {SDPA_MEAN_ABS:g}); |out| mean {sd.abs().mean():.3e}")
+    record(msg)
+    assert e.mean() < SDPA_MEAN_ABS, msg
+    assert e.max() < SDPA_MAX_ABS, msg
 
 
 def test_reference_cosine_gate():
@@ -352,8 +359,10 @@ def test_reference_cosine_gate():
     sd = _sdpa_gpu_fp32(q, k, v)
     cos = torch.nn.functional.cosine_similarity(out.flatten(), sd.flatten(), dim=0).item()
     e = (out - sd).abs()
-    print(f"cosine vs fp32 SDPA {cos:.6f} (reference INT8: 0.999246); max {e.max():.3e} mean {e.mean():.3e}")
-    assert cos >= 0.999246
+    msg = (f"q 6032 x kv 27144 randn: cosine vs fp32 SDPA {cos:.6f} (reference INT8 kernel: 0.999246); "
+           f"max {e.max():.3e} mean {e.mean():.3e}")
+    record(msg)
+    assert cos >= 0.999246, msg
 
 
 def test_graph_replay_matches_eager():
@@ -421,6 +430,25 @@ def test_attn_fwd_refuses_mismatched_buffers():
     with pytest.raises(ValueError):   # q8 holds 256 padded rows: 300 queries do not fit
         kernels.attn_fwd(q8, qs, None, 1, 300, 2, ring, 0, [0], [130],
                          torch.empty(1, 300, 2, 128, dtype=torch.bfloat16, device=DEV))
+    # Q quantised for a longer sequence (512 padded rows per head): the kernel would read head 1 at row 256 of
+    # head 0's rows
+    q_long = torch.randn(1, 300, 2, 128, device=DEV).to(torch.bfloat16)
+    q8l, qsl, _ = kernels.quant_q(q_long)
+    with pytest.raises(ValueError):
+        kernels.attn_fwd(q8l, qsl, None, 1, 100, 2, ring, 0, [0], [130], good)
+    with pytest.raises(ValueError):   # a non-contiguous view of the right shape
+        kernels.attn_fwd(q8l[:, :256], qsl[:, :8], None, 1, 100, 2, ring, 0, [0], [130], good)
+    with pytest.raises(ValueError):   # one chunk takes no bias
+        kernels.attn_fwd(q8, qs, torch.zeros(1, 2, 256, device=DEV), 1, 100, 2, ring, 0, [0], [130], good)
+    ring2 = _ring(1, 2, 130, slots=2)
+    kernels.kv_requant(k.to(DEV), v.to(DEV), ring2, 0)
+    kernels.kv_requant(k.to(DEV), v.to(DEV), ring2, 1)
+    for bad_bias in (None, torch.zeros(1, 2, 256, device=DEV), torch.zeros(2, 2, 100, device=DEV),
+                     torch.zeros(2, 2, 256, device=DEV, dtype=torch.float64)):
+        with pytest.raises(ValueError):   # two chunks need a (2, BH, Lp) bias: a smaller one is read past its end
+            kernels.attn_fwd(q8, qs, bad_bias, 1, 100, 2, ring2, 0, [0, 1], [130, 130], good)
+    q8b, qsb, bias = kernels.quant_q(q.to(DEV), "NHD", ring2, 0, [0, 1])
+    kernels.attn_fwd(q8b, qsb, bias, 1, 100, 2, ring2, 0, [0, 1], [130, 130], good)
     torch.cuda.synchronize()
 
 
@@ -476,3 +504,46 @@ def test_one_plane_path():
           f"{e_scheme.mean():.3e}")
     assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
     assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
+
+
+def test_reference_window_ring():
+    """The reference's token window (sink 6 frames, 18 frames in all, 4-frame chunks; kv_cache.py:23-81) at
+    50-token frames over 7 chunks: the last forward attends chunk 0, the first 100 tokens of chunk 1 (the rest of
+    the sink), chunks 4 and 5 and the current chunk 6 -- 900 keys in 5 slots -- and matches the oracle over exactly
+    those tokens (each chunk quantised whole, read as a prefix) and fp32 SDPA over the same bf16 keys."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    from oracle import kv_window
+    h, frame = 3, 50
+    n = 4 * frame
+    g = torch.Generator().manual_seed(66)
+    chunks = [((torch.randn(1, n, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16(),
+               (torch.randn(1, n, h, 128, generator=g) * (1 + 0.2 * i)).bfloat16()) for i in range(7)]
+    q = torch.randn(1, 250, h, 128, generator=g).bfloat16()
+    ring = QuantKVRing.from_frames(1, 1, h, frame, 4, 6, 18, device=DEV)
+    assert ring.slots == 5
+    for i, (kk, vv) in enumerate(chunks):
+        ring.write(0, kk.to(DEV), vv.to(DEV))
+        if i < 6:
+            ring.commit()
+    pos = ring.stream_positions()
+    assert pos == kv_window.rollout_positions([n] * 7, 1, 18 * frame, 6 * frame)[6][0].tolist()
+    slots, lens = ring.attended()
+    assert lens == [200, 100, 200, 200, 200]
+    out = ring.attend(q.to(DEV), 0).float().cpu()
+    used = [(0, 200), (1, 100), (4, 200), (5, 200), (6, 200)]
+    ref_chunks = []
+    for i, m in used:
+        c = emu.requant(*chunks[i])
+        c["n"] = m                       # the quantised chunk, read as a prefix
+        ref_chunks.append(c)
+    ref = emu.attention(q, ref_chunks, schedule_gx=_gx())[None]
+    kk = torch.cat([chunks[i][0][:, :m] for i, m in used], 1)
+    vv = torch.cat([chunks[i][1][:, :m] for i, m in used], 1)
+    assert pos == [i * n + t for i, m in used for t in range(m)] and kk.shape[1] == 900
+    sd = emu.sdpa_fp32(q, kk, vv)[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    record(f"reference window ring (sink 1.5 chunks, 900 keys) vs oracle mean {e_emu.mean():.3e}; vs fp32 SDPA "
+           f"max {e_sd.max():.3e} mean {e_sd.mean():.3e}; oracle vs SDPA mean {e_scheme.mean():.3e}")
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
+    assert e_sd.max() <= 2 * e_scheme.max() + 1e-3

@@ -265,3 +265,88 @@ def test_schedule_covers_every_block_once():
         for t in range(n_tiles):
             blocks = [j for j0, j1 in sched[t] for j in range(j0, j1)]
             assert blocks == list(range(nb)), (n_tiles, nb, gx, t)
+
+
+# ---------------------------------------------------------------- online softmax, chunk switches and split merge
+
+def _ragged_chunks(seed, lens=(200, 150, 333), h=2, lq=300):
+    """Chunks with their own K offsets (so the per-chunk means and the logit bias differ) and V amplitudes (so
+    the V scales differ, exercising the accumulator's rescale at each chunk switch)."""
+    g = torch.Generator().manual_seed(seed)
+    ks, vs = [], []
+    for i, n in enumerate(lens):
+        ks.append((torch.randn(1, n, h, 128, generator=g) + (2 + i) * torch.randn(1, 1, h, 128, generator=g))
+                  .to(torch.bfloat16))
+        vs.append((torch.randn(1, n, h, 128, generator=g) * (0.5, 1.0, 3.0)[i % 3]).to(torch.bfloat16))
+    q = torch.randn(1, lq, h, 128, generator=g).to(torch.bfloat16)
+    return q, ks, vs
+
+
+def _direct_softmax_fp64(q, chunks, sm_scale=None):
+    """Exact softmax attention of the dequantised logits and V in fp64, one row at a time in closed form:
+    logit = q8.k8 * q_scale * k_scale + q.km_c (several chunks), base-e softmax, O = sum P V v_scale / sum P.
+    No block order, no running max, no split: what the online form must equal when P is not rounded."""
+    q = q[0]
+    lq, h, d = q.shape
+    sm = d ** -0.5 if sm_scale is None else sm_scale
+    q8, qs = emu.quant_q(q)
+    qsr = qs.repeat_interleave(emu.Q_GROUP, dim=1).double()
+    out = torch.empty(lq, h, d, dtype=torch.float64)
+    for hh in range(h):
+        logits, vals = [], []
+        for c in chunks:
+            n = c["n"]
+            s = q8[hh, :lq].double() @ c["k8"][hh, :n].double().t()
+            s = s * qsr[hh, :lq, None] * c["k_scale"][hh].repeat_interleave(emu.K_BLOCK)[:n].double()[None, :]
+            if len(chunks) > 1:
+                s = s + (q[:, hh].double() @ c["km"][hh].double())[:, None]
+            logits.append(s * sm)
+            vals.append(emu.dequant_v(c)[hh].double() * c["v_scale"][hh].double()[None, :])
+        s = torch.cat(logits, dim=1)
+        p = torch.softmax(s, dim=1)
+        out[:, hh] = p @ torch.cat(vals, dim=0)
+    return out
+
+
+@pytest.mark.parametrize("gx", [None, 1, 2, 3, 8, 16])
+def test_online_split_and_chunk_switch_exact_without_p_rounding(gx):
+    """With P unrounded, the oracle's online softmax -- lazy running max, per-chunk bias, O rescaled by the V-scale
+    ratio at each chunk switch, tiles cut into pieces and merged -- must equal direct softmax attention of the same
+    dequantised logits and V to fp32 rounding. A dropped rescale, bias or merge weight is an O(1) error here."""
+    q, ks, vs = _ragged_chunks(31)
+    chunks = [emu.requant(k, v) for k, v in zip(ks, vs)]
+    want = _direct_softmax_fp64(q, chunks)
+    got = emu.attention(q, chunks, schedule_gx=gx, p_round=False).double()
+    if gx is not None:   # the schedule really cuts tiles: 4 tiles (2 heads x 2 query tiles) on 8 XCDs
+        sched = emu.attn_schedule(4, sum(-(-c["n"] // 64) for c in chunks), gx)
+        assert any(len(p) > 1 for p in sched.values()) == (gx > 1)
+    err = (got - want).abs().max().item()
+    assert err < 2e-5 * want.abs().max().item(), err
+
+
+def test_split_pieces_change_only_p_rounding():
+    """With P rounded to e4m3, cutting tiles into pieces moves each row's reference max, hence which e4m3 step a
+    P lands on: split and unsplit results are two draws of the same rounding noise, equally close to fp32 SDPA
+    (a wrong merge would add its own error on top)."""
+    q, ks, vs = _ragged_chunks(32)
+    chunks = [emu.requant(k, v) for k, v in zip(ks, vs)]
+    sd = emu.sdpa_fp32(q, torch.cat(ks, 1), torch.cat(vs, 1))
+    base = emu.attention(q, chunks)
+    e_base = (base - sd).abs().mean()
+    for gx in (2, 8, 16):
+        split = emu.attention(q, chunks, schedule_gx=gx)
+        assert (split - base).abs().mean() < 1.5 * e_base
+        assert 0.75 < (split - sd).abs().mean() / e_base < 1.33
+
+
+def test_multichunk_within_sdpa_tolerance_of_concatenated_keys():
+    """Four chunks with different K means and V amplitudes (per-chunk bias and V-scale ratio rescale), P rounded:
+    as close to fp32 SDPA over the concatenated bf16 keys as one chunk over the same keys."""
+    q, ks, vs = _ragged_chunks(33, lens=(640, 512, 700, 448), lq=256)
+    kk, vv = torch.cat(ks, 1), torch.cat(vs, 1)
+    sd = emu.sdpa_fp32(q, kk, vv)
+    multi = emu.attention(q, [emu.requant(k, v) for k, v in zip(ks, vs)])
+    single = emu.attention(q, [emu.requant(kk, vv)])
+    e_m, e_s = (multi - sd).abs(), (single - sd).abs()
+    assert e_m.max() < 1.25 * e_s.max()
+    assert e_m.mean() < 1.25 * e_s.mean() + 1e-5
