@@ -547,3 +547,72 @@ def test_reference_window_ring():
     assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
     assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
     assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
+
+
+def test_cfg5_chunk_graph_full_size():
+    """cfg 5 at full size: one HIP graph of a whole chunk -- 30 layers x 5 passes (4 denoising steps and the clean
+    pass, lingbot/pipelines/lingbot_world.py:460,510-553), each re-quantising that layer's current chunk and
+    attending Q [1,6032,12,128] over it plus 3 cached chunks (24128 keys), then the 30-layer save. Replays
+    reproduce the eager run bit for bit (outputs and ring); the saved slot of sampled layers is the oracle's
+    re-quant bit for bit; a layer's output is within the fp32-SDPA gates."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    layers, passes, n, h = 30, 5, 6032, 12
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    ring = QuantKVRing(layers, 1, h, n, slots=4, device=DEV)
+    mem = []
+    for _ in range(3):
+        mk = (torch.randn(1, n, h, 128, device=DEV, generator=gen) * 1.5).to(torch.bfloat16)
+        mv = (torch.randn(1, n, h, 128, device=DEV, generator=gen) * 1.5).to(torch.bfloat16)
+        for layer in range(layers):
+            ring.write(layer, mk, mv)
+        ring.commit()
+        mem.append((mk, mv))
+    q = torch.randn(1, n, h, 128, device=DEV, generator=gen).to(torch.bfloat16)
+    kl = (torch.randn(layers, 1, n, h, 128, device=DEV, generator=gen) +
+          3 * torch.randn(layers, 1, 1, h, 128, device=DEV, generator=gen)).to(torch.bfloat16)
+    vl = torch.randn(layers, 1, n, h, 128, device=DEV, generator=gen).to(torch.bfloat16)
+    outs = [torch.empty_like(q) for _ in range(layers)]
+    cur = ring.current
+
+    def chunk():
+        for _ in range(passes):
+            for layer in range(layers):
+                ring.write(layer, kl[layer], vl[layer])
+                outs[layer].copy_(ring.attend(q, layer))
+        ring.write_layers(kl, vl)
+
+    chunk()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    saved = [t[:, cur].clone() for t in (ring.cache.k8, ring.cache.k_scale, ring.cache.km, ring.cache.v8,
+                                         ring.cache.v8lo, ring.cache.v_scale)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        chunk()
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for o in outs:
+            o.fill_(float("nan"))
+        ring.cache.k8[:, cur].zero_()
+        ring.cache.v8[:, cur].zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for layer, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), f"replay {rep}: layer {layer} differs from the eager run"
+        for t, s in zip((ring.cache.k8, ring.cache.k_scale, ring.cache.km, ring.cache.v8, ring.cache.v8lo,
+                         ring.cache.v_scale), saved):
+            assert torch.equal(t[:, cur], s), f"replay {rep}: the saved slot differs from the eager run"
+    for layer in (0, 13, 29):
+        _check_chunk(ring.cache, layer, cur, emu.requant(kl[layer].cpu(), vl[layer].cpu()), n)
+    layer = 29
+    kk = torch.cat([m[0] for m in mem] + [kl[layer]], 1)
+    vv = torch.cat([m[1] for m in mem] + [vl[layer]], 1)
+    sd = _sdpa_gpu_fp32(q, kk, vv)
+    e = (outs[layer].float() - sd).abs()
+    msg = (f"cfg5 graph (30 layers x 5 passes + save), layer {layer} vs fp32 SDPA: max {e.max():.3e} "
+           f"(gate {SDPA_MAX_ABS:g}) mean {e.mean():.3e} (gate {SDPA_MEAN_ABS:g})")
+    record(msg)
+    assert e.max() < SDPA_MAX_ABS and e.mean() < SDPA_MEAN_ABS, msg
