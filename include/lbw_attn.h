@@ -46,7 +46,8 @@ enum {
   LBW_E_ALIGN = 3,       /* a pointer or stride breaks the 16-byte alignment the kernels load with */
   LBW_E_DEVICE = 4,      /* the current device is not gfx950 */
   LBW_E_LAUNCH = 5,      /* the kernel launch failed */
-  LBW_E_SEGMENTS = 6     /* the attended-chunk table is invalid */
+  LBW_E_SEGMENTS = 6,    /* the attended-chunk table is invalid */
+  LBW_E_SCRATCH = 7      /* the problem needs more scratch than lbw_attn_fwd_noalloc's fixed array holds */
 };
 
 #define LBW_HEAD_DIM 128
@@ -112,8 +113,30 @@ int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias,
                  float sm_scale, void* workspace, void* stream);
 
 /* Bytes of scratch lbw_attn_fwd needs on the current device (partial results of query tiles whose key range
- * is split between workgroups); independent of the problem size. */
+ * is split between workgroups); independent of the problem size. Calls that share a workspace must not overlap
+ * (calls on different streams need workspaces of their own). */
 int64_t lbw_attn_workspace_bytes(void);
+
+/*
+ * lbw_attn_fwd without the workspace argument, for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Has no counterpart in the reference.
+ * Same arguments (less `workspace`), kernels and results as lbw_attn_fwd; the split-tile partials go to a fixed
+ * array inside the library, one per GPU, of lbw_attn_noalloc_scratch_bytes() = 68,157,440 bytes (the workspace
+ * of a device with up to 256 CUs; LBW_E_SCRATCH on a larger one), held until the process ends. Allocates, frees
+ * and synchronises nothing. The first call on a device looks up that device's array (hipGetSymbolAddress): make
+ * it outside graph capture. Every call on one GPU shares its array, so calls that overlap on one GPU (on other
+ * streams or host threads) race on it.
+ */
+int lbw_attn_fwd_noalloc(const int8_t* q8, const float* q_scale, const float* bias,
+                         int64_t batch, int64_t lq, int64_t heads,
+                         const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
+                         const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                         const int32_t* seg_len,
+                         uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
+                         float sm_scale, void* stream);
+
+/* Size of lbw_attn_fwd_noalloc's per-GPU scratch array, in bytes. */
+int64_t lbw_attn_noalloc_scratch_bytes(void);
 
 /* Persistent workgroups per XCD that lbw_attn_fwd launches on the current device (one per CU). Query tiles
  * are dealt to XCDs in 8 contiguous ranges and, within one, whole tiles go round-robin to these workgroups

@@ -817,6 +817,45 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   return LBW_OK;
 }
 
+// ---- the entry point that allocates nothing -----------------------------------------------------------------
+// The split-tile partials of lbw_attn_fwd_noalloc live in this file-scope array instead of a caller workspace:
+// one copy per GPU, held until the process ends. Its size is the attention workspace at 32 workgroups per XCD
+// (256 CUs). In host code `scratch` names a host-side stand-in, never the device memory: the device address of a
+// GPU's copy comes from hipGetSymbolAddress on that GPU, once, and only that address is passed to kernels.
+constexpr int SCRATCH_WGS_PER_XCD = 32;
+constexpr int64_t ATTN_SCRATCH_BYTES = (int64_t)XCDS * SCRATCH_WGS_PER_XCD * 2 * QT * (D + 2) * (int64_t)sizeof(float);
+static __device__ __align__(256) uint8_t scratch[ATTN_SCRATCH_BYTES];
+
+// Device address of this GPU's `scratch` (the current device's), looked up on the first call on each device and
+// kept per device ordinal; null if the lookup fails.
+static void* scratch_on_current_device() {
+  static std::atomic<void*> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  void* p = cached[dev].load(std::memory_order_acquire);
+  if (!p) {
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    cached[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+extern "C" int64_t lbw_attn_noalloc_scratch_bytes(void) { return ATTN_SCRATCH_BYTES; }
+
+extern "C" int lbw_attn_fwd_noalloc(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
+                                    int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
+                                    const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
+                                    int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
+                                    uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
+                                    float sm_scale, void* stream) {
+  if (const int dv = check_device()) return dv;
+  if (lbw_attn_workspace_bytes() > ATTN_SCRATCH_BYTES) return LBW_E_SCRATCH;   // more CUs than the array covers
+  void* ws = scratch_on_current_device();
+  if (!ws) return LBW_E_DEVICE;
+  return lbw_attn_fwd(q8, q_scale, bias, batch, lq, heads, k8, k_scale, v8, v8lo, v_scale, slots, cap, n_seg,
+                      seg_slot, seg_len, out, o_s_batch, o_s_tok, o_s_head, sm_scale, ws, stream);
+}
+
 extern "C" int lbw_qk_logits_i32(const int8_t* q8, int64_t bh, int64_t lq, const int8_t* k8, int64_t slots,
                                  int64_t cap, int64_t slot, int32_t* out, void* stream) {
   if (!q8 || !k8 || !out) return LBW_E_NULL;

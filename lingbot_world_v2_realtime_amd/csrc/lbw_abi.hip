@@ -13,6 +13,7 @@ extern "C" const char* lbw_status_string(int status) {
     case LBW_E_DEVICE: return "device is not gfx950";
     case LBW_E_LAUNCH: return "kernel launch failed";
     case LBW_E_SEGMENTS: return "bad chunk table";
+    case LBW_E_SCRATCH: return "problem exceeds the fixed scratch array";
     default: return "unknown status";
   }
 }

@@ -148,9 +148,10 @@ def attn_workspace(device, stream=None):
 
 
 def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_lens, out, layout="NHD",
-             sm_scale=None, workspace=None):
+             sm_scale=None, workspace=None, noalloc=False):
     """Quantized attention of quantised Q over the chunks `seg_slots` (with `seg_lens` valid tokens) of one
-    layer of `ring`, written into bf16 `out` ([B, Lq, H, 128] NHD or [B, H, Lq, 128] HND)."""
+    layer of `ring`, written into bf16 `out` ([B, Lq, H, 128] NHD or [B, H, Lq, 128] HND). noalloc=True calls
+    lbw_attn_fwd_noalloc, whose scratch is the library's fixed per-GPU array (no workspace)."""
     lib = _lib.load()
     n_seg = len(seg_slots)
     if not 1 <= n_seg <= MAX_SEGMENTS or len(seg_lens) != n_seg:
@@ -179,6 +180,12 @@ def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_le
     k8, ksc, _, v8, v8lo, vsc = ring.layer_view(layer)
     slot_arr = (ctypes_i32 * n_seg)(*seg_slots)
     len_arr = (ctypes_i32 * n_seg)(*seg_lens)
+    if noalloc:
+        st = lib.lbw_attn_fwd_noalloc(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
+                                      _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr,
+                                      _ptr(out), o_b, o_t, o_h, sm_scale, _stream(q8))
+        _lib.check(st, "lbw_attn_fwd_noalloc")
+        return out
     if workspace is None:
         workspace = attn_workspace(q8.device, _stream(q8))
     st = lib.lbw_attn_fwd(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),

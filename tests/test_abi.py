@@ -13,7 +13,7 @@ from lingbot_world_v2_realtime_amd import _lib
 
 HEADER = os.path.join(os.path.dirname(__file__), "..", "include", "lbw_attn.h")
 
-OK, E_NULL, E_SHAPE, E_ALIGN, E_DEVICE, E_LAUNCH, E_SEGMENTS = range(7)
+OK, E_NULL, E_SHAPE, E_ALIGN, E_DEVICE, E_LAUNCH, E_SEGMENTS, E_SCRATCH = range(8)
 FAKE = 1 << 20          # a 16-byte aligned non-null address; never dereferenced on the paths tested here
 
 
@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declarations_are_bound_and_exported(lib):
     decl = declared_functions()
-    assert len(decl) == 9
+    assert len(decl) == 11
     assert set(decl) == set(_lib.SIGNATURES)
     for name, n in decl.items():
         assert len(_lib.SIGNATURES[name][1]) == n, name
@@ -47,10 +47,15 @@ def test_header_declarations_are_bound_and_exported(lib):
 
 
 def test_status_strings_and_version(lib):
-    names = [lib.lbw_status_string(s).decode() for s in range(7)]
-    assert names[0] == "ok" and len(set(names)) == 7
+    names = [lib.lbw_status_string(s).decode() for s in range(8)]
+    assert names[0] == "ok" and len(set(names)) == 8 and "unknown status" not in names
     assert lib.lbw_status_string(99).decode() == "unknown status"
     assert lib.lbw_version() == 100
+
+
+def test_noalloc_scratch_size(lib):
+    # the attention workspace of 8 XCDs x 32 workgroups: 2 partial slots of 256 rows x (128 channels + m, l)
+    assert lib.lbw_attn_noalloc_scratch_bytes() == 8 * 32 * 2 * 256 * 130 * 4 == 68_157_440
 
 
 def test_requant_workspace_formula(lib):
@@ -161,6 +166,10 @@ def test_valid_call_without_gfx950_is_refused(lib):
     assert requant(lib) == E_DEVICE
     assert quant_q(lib) == E_DEVICE
     assert attn(lib) == E_DEVICE
+    seg = (ctypes.c_int32 * 1)(0)
+    ln = (ctypes.c_int32 * 1)(100)
+    assert lib.lbw_attn_fwd_noalloc(FAKE, FAKE, None, 1, 100, 2, FAKE, FAKE, FAKE, None, FAKE, 1, 128, 1, seg, ln,
+                                    FAKE, 0, 256, 128, 0.088, None) == E_DEVICE
     assert lib.lbw_qk_logits_i32(FAKE, 2, 100, FAKE, 1, 128, 0, FAKE, None) == E_DEVICE
 
 
