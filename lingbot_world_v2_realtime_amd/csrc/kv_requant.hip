@@ -4,9 +4,9 @@
 //   1. kv_stats:    per 64-token block (grid: block, batch*head, layer), fp32 column sums of K and column max |V|
 //                   (K and V read once).
 //   2. kv_finalize: per (batch*head, layer, 16 channels), the block partials summed into 4-block super-blocks
-//                   in parallel, the super-blocks left to right, then the mean -> bf16, the V scale and its
-//                   reciprocal.
-//   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * (448 / amax) -> e4m3 hi = rn(y) and, when a
+//                   in parallel, the super-blocks left to right, then the mean -> bf16, the V scale (the power of
+//                   two 2^e with amax / 2^e in (224, 448]) and its reciprocal.
+//   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * 2^-e (exact) -> e4m3 hi = rn(y) and, when a
 //                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K and
 //                   V a second time).
 // The column-sum order is fixed (see the oracle's chunk_mean): s = x[4q] + x[4q+1] + x[4q+2] + x[4q+3] per
@@ -124,8 +124,12 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
     mx = fmaxf(mx, AMAX_FLOOR);
     const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + ch;
     km[so] = bf16_round(__fdiv_rn(tot, (float)a.len));
-    v_scale[so] = __fdiv_rn(mx, V_MAX);
-    v_recip[grp * D + ch] = __fdiv_rn(V_MAX, mx);
+    // amax = f * 2^x with f in [0.5, 1) (mx is a normal float): 2^e takes it into (224, 448] = (0.875 * 2^8,
+    // 0.875 * 2^9] with e = x - 9 when f <= 0.875 (mantissa bits <= 0x600000), else x - 8; x = biased exponent - 126
+    const uint32_t mb = __float_as_uint(mx);
+    const int e = (int)(mb >> 23) - ((mb & 0x7FFFFFu) <= 0x600000u ? 135 : 134);
+    v_scale[so] = __uint_as_float((uint32_t)(127 + e) << 23);
+    v_recip[grp * D + ch] = __uint_as_float((uint32_t)(127 - e) << 23);
   }
 }
 

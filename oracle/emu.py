@@ -12,13 +12,17 @@ quantisers and its documentation of the fused kernel:
   tensor is (lingbot/layers/sage_preq.py:115; sage_kvq.py:85, :96), then int8 per 64-token block as above;
   tokens past the chunk count as zero after the subtraction (sage_kvq.py:61-63).
 - V: fp8 e4m3 with one scale per (head, channel) (sage_kvq.py:69-75; sage_preq.py:47-78). The reference maps
-  amax to 2.25 because its PV accumulates in fp16 (sage_kvq.py:30-31); the MFMA here accumulates in fp32,
-  so amax maps to the full e4m3 range 448. Values are clamped first because torch's fp32 -> e4m3 cast is
-  round-to-nearest-even but not saturating.
+  amax to 2.25 because its PV accumulates in fp16 (sage_kvq.py:30-31); the MFMA here accumulates in fp32, so
+  the scale is the power of two 2^e that takes amax into (224, 448], the top binade of e4m3: V / 2^e is exact,
+  e4m3's relative precision is the same in every binade, and a power-of-two scale can ride on the fp8 MFMA's
+  E8M0 block-scale operand instead of a multiply of the accumulator.
 - Logits: S = q8 . k8 in int32 (experiments/bench_attn/h2_tiles/README.md:45), dequantised with
   q_scale * k_scale * sm_scale * log2(e) into the exp2 domain; P = exp2(s - m + 8.807) <= 448 cast to e4m3
-  (experiments/bench_attn/phi_calib.md:11-16); O = sum P V / sum P, times the V scale
-  (h2_tiles/README.md:13-20; experiments/bench_attn/splitkv/README.md:62-63).
+  (experiments/bench_attn/phi_calib.md:11-16); O = sum P V / sum P, with the V scale
+  (h2_tiles/README.md:13-20; experiments/bench_attn/splitkv/README.md:62-63). The reference max m of a row
+  moves only when a block's max passes it by more than RESCALE_SLACK, so the rescale of the accumulated O is
+  rare; each block's contribution is accumulated in true V units (its chunk's power-of-two V scale applied), so
+  a switch between chunks with different V scales needs no rescale.
 - Memory chunks keep their own mean and V scale; the bias q . mean_c of chunk c is added to its logits
   (a constant per (query, chunk), so it drops out when there is only one chunk).
 
@@ -153,18 +157,23 @@ def quant_k(k, km):
 
 
 def v_scale_of(v):
-    """v bf16 [L, H, D] -> (v_scale, recip) fp32 [H, D]: amax / 448 and 448 / amax, amax floored at 1e-7."""
+    """v bf16 [L, H, D] -> (v_scale, recip) fp32 [H, D]: the power of two 2^e with amax / 2^e in (224, 448]
+    (amax floored at 1e-7), and 2^-e. With amax = f * 2^x, f in [0.5, 1): e = x - 9 when f <= 0.875 (448 =
+    0.875 * 2^9), else x - 8 -- integer arithmetic on the exponent, no rounding."""
     v = _as_lhd(v)
     amax = v.float().abs().amax(dim=0).clamp_min(AMAX_FLOOR)
-    vmax = torch.full_like(amax, V_MAX)
-    return amax / vmax, vmax / amax
+    f, x = torch.frexp(amax)
+    e = torch.where(f <= 0.875, x - 9, x - 8)
+    one = torch.ones_like(amax)
+    return torch.ldexp(one, e), torch.ldexp(one, -e)
 
 
 def quant_v(v):
     """v bf16 [L, H, D] -> (v8, v8lo uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, v_scale fp32 [H, D]).
 
-    Two e4m3 terms: y = v * (448 / amax); hi = e4m3(y); lo = e4m3((y - hi) * 16), so v ~ (hi + lo / 16) * v_scale.
-    y - hi is exact in fp32 (hi is y rounded to 3 mantissa bits) and |y - hi| * 16 <= 256 stays in range."""
+    Two e4m3 terms: y = v / v_scale (exact: a power of two, |y| <= 448); hi = e4m3(y); lo = e4m3((y - hi) * 16),
+    so v ~ (hi + lo / 16) * v_scale. y - hi is exact in fp32 (hi is y rounded to 3 mantissa bits) and
+    |y - hi| * 16 <= 256 stays in range."""
     v = _as_lhd(v)
     n, h, d = v.shape
     lp = pad_to(n, K_BLOCK)
@@ -249,14 +258,14 @@ def attn_schedule(n_tiles, nb, gx):
 
 def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=None, p_round=True):
     """Online softmax over tile-relative key blocks [j0, j1) (numbered across the chunks in order) for the
-    query rows `qf` (q8 as fp32) -> (o in units of the last chunk's V scale, m, l, last chunk index).
-    The reference max m of a row moves only when a block's max exceeds it by more than `tau`. With
-    p_round=False, P enters the PV product unrounded (fp32) instead of as e4m3."""
+    query rows `qf` (q8 as fp32) -> (o in true V units, m, l). The reference max m of a row moves only when a
+    block's max exceeds it by more than `tau`. With p_round=False, P enters the PV product unrounded (fp32)
+    instead of as e4m3."""
     rows, d = qf.shape[0], qf.shape[1]
     m_run = torch.full((rows,), float("-inf"))
     l_run = torch.zeros(rows)
     o = torch.zeros(rows, d)
-    vs_prev, c_last, j = None, None, 0
+    j = 0
     for ci, c in enumerate(chunks):
         n = c["n"]
         nbc = pad_to(n, K_BLOCK) // K_BLOCK
@@ -264,8 +273,6 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
             j += nbc
             continue
         vs = c["v_scale"][hh]
-        if vs_prev is not None:
-            o = o * (vs_prev / vs)[None, :]
         beta = beta_of(ci)
         for b in range(max(0, j0 - j), min(nbc, j1 - j)):
             k0, k1 = b * K_BLOCK, min(n, b * K_BLOCK + K_BLOCK)
@@ -283,10 +290,11 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
             x = (s_int.double() * cb.double()[:, None] + kc[:, None]).float()
             p = torch.exp2(x)
             l_run = l_run + p.sum(dim=1)
-            o = o + torch.matmul(e4m3_decode(e4m3_encode(p)) if p_round else p, vdec[ci][hh, k0:k1])
-        vs_prev, c_last = vs, ci
+            pr = e4m3_decode(e4m3_encode(p)) if p_round else p
+            # the chunk's V scale is a power of two: exact, and the same factor the MFMA's block scale applies
+            o = o + torch.matmul(pr, vdec[ci][hh, k0:k1]) * vs[None, :]
         j += nbc
-    return o, m_run, l_run, c_last
+    return o, m_run, l_run
 
 
 def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None, stats=None, p_round=True):
@@ -294,9 +302,9 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
     kernel's own order: chunks in sequence, 64-key blocks in sequence, a reference row max m, and per block
       b = max_j S_ij * cb + beta,  m_new = b if b > m + tau else m,  alpha = exp2(m - m_new),
       o = alpha * o,  l = alpha * l,  P_ij = exp2(S_ij * cb + beta - m_new + 8.807 - tau)  (<= 448),
-      l += sum P,  o += e4m3(P) . V8,
-    with cb = q_scale * k_scale * sm_scale * log2(e); at a chunk boundary o is rescaled by
-    v_scale_old / v_scale_new per channel; finally out = o * v_scale / l.
+      l += sum P,  o += (e4m3(P) . V8) * v_scale,
+    with cb = q_scale * k_scale * sm_scale * log2(e) and beta = q . mean_k of the chunk (several chunks only);
+    finally out = o / l. Each block's contribution is in true V units, so a chunk switch needs no rescale.
     With `schedule_gx` (the kernel's workgroups per XCD), tiles the kernel splits between workgroups are
     computed piece by piece from a fresh state and merged by `merge_partials`.
     p_round=False skips the e4m3 rounding of P (a checking mode: the result is then exact softmax attention of
@@ -340,13 +348,11 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
             qsr = qsr_all[hh, a:e]
             beta_of = (lambda ci: bias[ci][hh, a:e]) if multi else (lambda ci: torch.zeros(e - a))
             if t is None:
-                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, 0, nb, sl2, tau, stats, p_round)
-                out[a:e, hh] = (o * chunks[cl]["v_scale"][hh][None, :]) * (1.0 / l)[:, None]
+                o, m, l = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, 0, nb, sl2, tau, stats, p_round)
+                out[a:e, hh] = o * (1.0 / l)[:, None]
                 continue
-            parts = []
-            for j0, j1 in sched[hh * q_tiles + t]:
-                o, m, l, cl = _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats, p_round)
-                parts.append((o * chunks[cl]["v_scale"][hh][None, :], m, l))
+            parts = [_attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats, p_round)
+                     for j0, j1 in sched[hh * q_tiles + t]]
             out[a:e, hh] = merge_partials(parts)
     return out
 

@@ -149,6 +149,22 @@ def test_smoothing_makes_k8_invariant_to_channel_offsets():
 
 # ---------------------------------------------------------------- V planes and layout
 
+def test_v_scale_power_of_two_edges():
+    """The exponent rule at the binade edges: amax exactly 448 * 2^e keeps e; one bf16 step above moves to e + 1;
+    an all-zero channel uses the 1e-7 floor."""
+    vals = torch.tensor([448.0, 450.0, 224.0, 225.0, 1.0, 3.5, 0.0])   # 450: the bf16 value after 448
+    v = torch.zeros(4, 1, len(vals))
+    v[1, 0] = vals
+    vs, recip = emu.v_scale_of(v.to(torch.bfloat16))
+    want = [1.0, 2.0, 0.5, 1.0, 2.0 ** -8, 2.0 ** -7, None]   # 3.5 = 448 * 2^-7 exactly
+    for got, w, a in zip(vs[0].tolist(), want, vals.tolist()):
+        if w is not None:
+            assert got == w, (a, got, w)
+    floor_scale = vs[0, -1].item()
+    assert 224 < 1e-7 / floor_scale <= 448
+    assert torch.all(vs * recip == 1)
+
+
 def test_v_position_map_is_a_bijection():
     assert sorted(emu.V_KEY_OF_POS.tolist()) == list(range(64))
     assert np.array_equal(emu.V_POS_OF_KEY[emu.V_KEY_OF_POS], np.arange(64))
@@ -161,8 +177,11 @@ def test_v_quant_layout_and_two_term_bound():
     v8, v8lo, vs = emu.quant_v(v)
     assert v8.shape == (h, 3, 128, 64)
     amax = v.float().abs().amax(dim=0)
-    assert torch.equal(vs, amax / torch.full_like(amax, 448.0))
-    y = v.float().permute(1, 0, 2) * (torch.full_like(amax, 448.0) / amax)[:, None, :]   # [h, n, d]
+    # the scale is a power of two taking the channel max into e4m3's top binade (224, 448]
+    mant, _ = torch.frexp(vs)
+    assert torch.all(mant == 0.5)
+    assert torch.all(amax / vs <= 448) and torch.all(amax / vs > 224)
+    y = v.float().permute(1, 0, 2) / vs[:, None, :]   # [h, n, d], exact
     chunk = {"v8": v8, "v8lo": v8lo, "n": n}
     one = emu.dequant_v(chunk, terms=1)
     two = emu.dequant_v(chunk, terms=2)
@@ -173,9 +192,10 @@ def test_v_quant_layout_and_two_term_bound():
     tol2 = torch.maximum(y.abs() * 2.0 ** -8, torch.full_like(y, 2.0 ** -13))
     assert torch.all((two - y).abs() <= tol2)
     assert (two - y).abs().mean() < (one - y).abs().mean() / 8
-    # the channel max lands exactly on 448
+    # the channel max lands in the top binade
     pos = y.abs().argmax(dim=1)
-    assert torch.all(one.gather(1, pos[:, None, :]).abs() == 448)
+    top = one.gather(1, pos[:, None, :]).abs()
+    assert torch.all(top >= 224) and torch.all(top <= 448)
 
 
 # ---------------------------------------------------------------- logits
