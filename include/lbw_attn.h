@@ -94,6 +94,42 @@ int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
                 void* stream);
 
 /*
+ * The self-attention prologue of a DiT block for Q, fused with its quantisation: q [batch][lq][heads * 128] bf16
+ * projection rows (strides s_batch, s_tok; channels contiguous) -> RMSNorm over all heads * 128 channels times
+ * norm_weight (bf16, heads * 128) with eps -> 3-axis rotary embedding -> the outputs of lbw_quant_q on that roped Q
+ * (q8, q_scale and, when n_seg > 1, bias; same layouts and conditions), plus the roped bf16 Q itself in q_out
+ * [batch][lq][heads][128] (strides o_s_*) when q_out is not null. Replaces norm_q + causal_rope_apply + the Q
+ * quantisation (lingbot/models/lingbot_world/transformer.py:201-211 with lingbot/layers/sage_preq.py:116).
+ * rope: float64 (cos, sin) table [rope_rows][64][2] (the model's freqs, transformer.py:553-556), 16-byte aligned;
+ * token t takes frame row start_frame + t / (grid_h grid_w) for pairs 0..21, row (t / grid_w) % grid_h for pairs
+ * 22..42 and row t % grid_w for pairs 43..63 (causal_rope_freqs, transformer.py:53-77). heads <= 16.
+ */
+int lbw_norm_rope_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
+                          int64_t s_batch, int64_t s_tok, const uint16_t* norm_weight, float eps,
+                          const double* rope, int64_t rope_rows, int64_t grid_h, int64_t grid_w,
+                          int64_t start_frame, int8_t* q8, float* q_scale,
+                          const float* km, int64_t slots, int n_seg, const int32_t* seg_slot, float* bias,
+                          uint16_t* q_out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head, void* stream);
+
+/*
+ * The same prologue for K, fused with the chunk's re-quant: k [batch][len][heads * 128] bf16 projection rows ->
+ * RMSNorm (norm_weight, eps) -> rotary embedding (rope table and grid as above) -> the roped bf16 K in k_out
+ * [batch][len][heads][128] (strides o_s_*), and the ring slot exactly as lbw_kv_requant (one layer) writes it from
+ * that roped K and v [batch][len][heads][128] (strides v_s_*). The K statistics are taken while the roped rows
+ * are in registers, so the roped K is read back once (by the quantiser) instead of twice. `workspace` holds
+ * lbw_kv_requant_workspace_bytes(1, batch * heads, len) bytes. Replaces norm_k + causal_rope_apply + kvc.write +
+ * the K/V quantisation (transformer.py:202-218; experiments/modules/sage_kvq.py:78-98).
+ */
+int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, int64_t batch, int64_t len, int64_t heads,
+                             int64_t k_s_batch, int64_t k_s_tok, int64_t v_s_batch, int64_t v_s_tok,
+                             int64_t v_s_head, const uint16_t* norm_weight, float eps,
+                             const double* rope, int64_t rope_rows, int64_t grid_h, int64_t grid_w,
+                             int64_t start_frame, uint16_t* k_out, int64_t o_s_batch, int64_t o_s_tok,
+                             int64_t o_s_head, int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo,
+                             float* v_scale, int64_t slots, int64_t cap, int64_t slot, void* workspace,
+                             void* stream);
+
+/*
  * Quantized attention of Q (from lbw_quant_q) over the chunks seg_slot[0..n_seg) of one layer's cache
  * (pointers already offset to that layer), chunk c holding seg_len[c] valid tokens (1..cap). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the

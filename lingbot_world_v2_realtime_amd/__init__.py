@@ -7,6 +7,6 @@ Python call surface (lingbot/layers/attention.py).
 """
 from . import _lib  # noqa: F401
 from .layers.attention import attention, flash_attention, sage_attention  # noqa: F401
-from .layers import kv_quant  # noqa: F401
+from .layers import kv_quant, prologue  # noqa: F401
 
-__all__ = ["attention", "flash_attention", "sage_attention", "kv_quant"]
+__all__ = ["attention", "flash_attention", "sage_attention", "kv_quant", "prologue"]

@@ -2,16 +2,17 @@
 //
 // Three launches:
 //   1. kv_stats:    per 64-token block (grid: block, batch*head, layer), fp32 column sums of K and column max |V|
-//                   (K and V read once).
-//   2. kv_finalize: per (batch*head, layer, 16 channels), the block partials summed into 4-block super-blocks
-//                   in parallel, the super-blocks left to right, then the mean -> bf16, the V scale (the power of
+//                   of each 32-token half (K and V read once).
+//   2. kv_finalize: per (batch*head, layer, 16 channels), the half-block partials summed into blocks and 4-block
+//                   super-blocks in parallel, the super-blocks left to right, then the mean -> bf16, the V scale (the power of
 //                   two 2^e with amax / 2^e in (224, 448]) and its reciprocal.
 //   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * 2^-e (exact) -> e4m3 hi = rn(y) and, when a
 //                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K and
 //                   V a second time).
 // The column-sum order is fixed (see the oracle's chunk_mean): s = x[4q] + x[4q+1] + x[4q+2] + x[4q+3] per
-// thread, q = 0..15 left to right per block, the blocks of each 4-block super-block left to right, then the
-// super-blocks left to right, so the mean is the same bits on every run and on the CPU.
+// thread, q = 0..7 and q = 8..15 left to right per half-block, the two halves added, the blocks of each 4-block
+// super-block left to right, then the super-blocks left to right, so the mean is the same bits on every run and
+// on the CPU. (The halves let a producer that sees 32 tokens at a time write the partials itself.)
 #include <algorithm>
 
 #include "lbw_common.h"
@@ -67,14 +68,15 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
     s_max[q][cg * 8 + c] = m[c];
   }
   __syncthreads();
-  if (t < D) {
+  {   // thread t: half t >> 7 of the block, channel t & 127
+    const int c = t & (D - 1), r0 = (t >> 7) * 8;
     float acc = 0.f, mx = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      acc = __fadd_rn(acc, s_sum[r][t]);
-      mx = fmaxf(mx, s_max[r][t]);
+    for (int r = 0; r < 8; ++r) {
+      acc = __fadd_rn(acc, s_sum[r0 + r][c]);
+      mx = fmaxf(mx, s_max[r0 + r][c]);
     }
-    const int64_t o = (((int64_t)layer * a.bh + bh) * a.nb + blk) * D + t;
+    const int64_t o = ((((int64_t)layer * a.bh + bh) * a.nb + blk) * 2 + (t >> 7)) * D + c;
     part_sum[o] = acc;
     part_amax[o] = mx;
   }
@@ -94,8 +96,8 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
   const int bh = blockIdx.x, layer = blockIdx.y, cgrp = blockIdx.z;
   const int t = threadIdx.x, c = t & (FIN_CH - 1), j = t / FIN_CH, ch = cgrp * FIN_CH + c;
   const int64_t grp = (int64_t)layer * a.bh + bh;
-  const float* bsum = part_sum + grp * a.nb * D + ch;
-  const float* bmax = part_amax + grp * a.nb * D + ch;
+  const float* bsum = part_sum + grp * a.nb * 2 * D + ch;   // [block][half][channel]
+  const float* bmax = part_amax + grp * a.nb * 2 * D + ch;
   const int nsup = (int)((a.nb + REQ_SUPER - 1) / REQ_SUPER);
   float tot = 0.f, mx = 0.f;
   for (int u0 = 0; u0 < nsup; u0 += FIN_U * FIN_J) {
@@ -106,8 +108,9 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
 #pragma unroll
       for (int i = 0; i < REQ_SUPER; ++i) {
         const bool ok = b0 + i < a.nb;
-        us = __fadd_rn(us, ok ? bsum[(int64_t)(b0 + i) * D] : 0.f);
-        mx = fmaxf(mx, ok ? bmax[(int64_t)(b0 + i) * D] : 0.f);
+        const int64_t o = (int64_t)(b0 + i) * 2 * D;
+        us = __fadd_rn(us, ok ? __fadd_rn(bsum[o], bsum[o + D]) : 0.f);
+        mx = fmaxf(mx, ok ? fmaxf(bmax[o], bmax[o + D]) : 0.f);
       }
       buf[uu * FIN_CH + c] = us;
     }
@@ -231,6 +234,50 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
   }
 }
 
+int kv_requant_check(int64_t layers, int64_t batch, int64_t len, int64_t heads, const int8_t* k8,
+                     const float* k_scale, const float* km, const uint8_t* v8, const uint8_t* v8lo,
+                     const float* v_scale, int64_t slots, int64_t cap, int64_t slot) {
+  if (!k8 || !k_scale || !km || !v8 || !v_scale) return LBW_E_NULL;
+  if (layers <= 0 || batch <= 0 || heads <= 0 || len <= 0 || slots <= 0 || cap <= 0) return LBW_E_SHAPE;
+  if (cap % KB != 0 || len > cap || slot < 0 || slot >= slots) return LBW_E_SHAPE;
+  if (layers > 65535 || batch * heads > 65535 || cap / KB > (int64_t)1 << 30) return LBW_E_SHAPE;
+  if (((uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo) & 15) return LBW_E_ALIGN;
+  return LBW_OK;
+}
+
+int kv_requant_launch(bool with_stats, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
+                      int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok,
+                      int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
+                      int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,
+                      int64_t slots, int64_t cap, int64_t slot, void* workspace, void* stream) {
+  if (!k || !v || !workspace) return LBW_E_NULL;
+  if (const int st = kv_requant_check(layers, batch, len, heads, k8, k_scale, km, v8, v8lo, v_scale, slots, cap,
+                                      slot))
+    return st;
+  const int64_t strides[8] = {k_s_layer, k_s_batch, k_s_tok, k_s_head, v_s_layer, v_s_batch, v_s_tok, v_s_head};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return LBW_E_ALIGN;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)workspace) & 15) return LBW_E_ALIGN;
+  ReqArgs a;
+  a.len = len; a.heads = heads; a.bh = batch * heads; a.slots = slots; a.cap = cap; a.slot = slot;
+  a.nb = (len + KB - 1) / KB;
+  a.nbc = cap / KB;
+  a.k_sl = k_s_layer; a.k_sb = k_s_batch; a.k_st = k_s_tok; a.k_sh = k_s_head;
+  a.v_sl = v_s_layer; a.v_sb = v_s_batch; a.v_st = v_s_tok; a.v_sh = v_s_head;
+  float* part_sum = (float*)workspace;
+  float* part_amax = part_sum + layers * a.bh * a.nb * 2 * D;
+  float* v_recip = part_amax + layers * a.bh * a.nb * 2 * D;
+  if (const int dv = check_device()) return dv;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
+  if (with_stats) hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
+  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers, D / FIN_CH), dim3(256), 0, st, a,
+                     part_sum, part_amax, v_recip, km, v_scale);
+  hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
+  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
+  return LBW_OK;
+}
+
 }  // namespace lbw
 
 using namespace lbw;
@@ -238,7 +285,7 @@ using namespace lbw;
 extern "C" int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len) {
   if (layers <= 0 || bh <= 0 || len <= 0) return 0;
   const int64_t nb = (len + KB - 1) / KB;
-  return (2 * layers * bh * nb * D + layers * bh * D) * (int64_t)sizeof(float);
+  return (4 * layers * bh * nb * D + layers * bh * D) * (int64_t)sizeof(float);
 }
 
 extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
@@ -247,32 +294,7 @@ extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t laye
                               int64_t v_s_tok, int64_t v_s_head, int8_t* k8, float* k_scale, float* km,
                               uint8_t* v8, uint8_t* v8lo, float* v_scale, int64_t slots, int64_t cap,
                               int64_t slot, void* workspace, void* stream) {
-  if (!k || !v || !k8 || !k_scale || !km || !v8 || !v_scale || !workspace) return LBW_E_NULL;
-  if (layers <= 0 || batch <= 0 || heads <= 0 || len <= 0 || slots <= 0 || cap <= 0) return LBW_E_SHAPE;
-  if (cap % KB != 0 || len > cap || slot < 0 || slot >= slots) return LBW_E_SHAPE;
-  if (layers > 65535 || batch * heads > 65535 || cap / KB > (int64_t)1 << 30) return LBW_E_SHAPE;
-  const int64_t strides[8] = {k_s_layer, k_s_batch, k_s_tok, k_s_head, v_s_layer, v_s_batch, v_s_tok, v_s_head};
-  for (int64_t s : strides)
-    if (s % 8 != 0) return LBW_E_ALIGN;
-  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo | (uintptr_t)workspace) & 15)
-    return LBW_E_ALIGN;
-  ReqArgs a;
-  a.len = len; a.heads = heads; a.bh = batch * heads; a.slots = slots; a.cap = cap; a.slot = slot;
-  a.nb = (len + KB - 1) / KB;
-  a.nbc = cap / KB;
-  a.k_sl = k_s_layer; a.k_sb = k_s_batch; a.k_st = k_s_tok; a.k_sh = k_s_head;
-  a.v_sl = v_s_layer; a.v_sb = v_s_batch; a.v_st = v_s_tok; a.v_sh = v_s_head;
-  float* part_sum = (float*)workspace;
-  float* part_amax = part_sum + layers * a.bh * a.nb * D;
-  float* v_recip = part_amax + layers * a.bh * a.nb * D;
-  if (const int dv = check_device()) return dv;
-  hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
-  hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
-  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers, D / FIN_CH), dim3(256), 0, st, a,
-                     part_sum,
-                     part_amax, v_recip, km, v_scale);
-  hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
-  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
-  return LBW_OK;
+  return kv_requant_launch(true, k, v, layers, batch, len, heads, k_s_layer, k_s_batch, k_s_tok, k_s_head,
+                           v_s_layer, v_s_batch, v_s_tok, v_s_head, k8, k_scale, km, v8, v8lo, v_scale, slots,
+                           cap, slot, workspace, stream);
 }

@@ -69,6 +69,18 @@ __device__ __forceinline__ float wave_max(float x) {
 // LBW_OK when the current device is a gfx950, else LBW_E_DEVICE (defined in lbw_abi.hip).
 int check_device();
 
+// The K/V re-quant's argument checks of the ring side, and its launches (kv_requant.hip). With with_stats false
+// the statistics pass is skipped: the caller has written its partials (column sums of K and column max |V| of each
+// 32-token half of each 64-token block, [layers][batch * heads][blocks][2][128] each) at the start of the workspace.
+int kv_requant_check(int64_t layers, int64_t batch, int64_t len, int64_t heads, const int8_t* k8,
+                     const float* k_scale, const float* km, const uint8_t* v8, const uint8_t* v8lo,
+                     const float* v_scale, int64_t slots, int64_t cap, int64_t slot);
+int kv_requant_launch(bool with_stats, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
+                      int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok,
+                      int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
+                      int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,
+                      int64_t slots, int64_t cap, int64_t slot, void* workspace, void* stream);
+
 // Position of key k (0..63) inside a 64-key fp8 V block.
 __device__ __forceinline__ int v_pos_of_key(int k) {
   return 32 * ((k >> 2) & 1) + 16 * ((k >> 5) & 1) + 4 * ((k >> 3) & 3) + (k & 3);

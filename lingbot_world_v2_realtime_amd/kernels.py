@@ -129,6 +129,87 @@ def quant_q(q, layout="NHD", ring=None, layer=0, seg_slots=()):
     return q8, qs, bias
 
 
+def _require_rows(name, x, heads):
+    """A projection [B, L, heads * 128] bf16 on the device with contiguous channels."""
+    if not x.is_cuda:
+        raise ValueError(f"{name} must be a device tensor (the quantized path has no CPU implementation)")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {x.dtype}")
+    if x.dim() != 3 or x.shape[-1] != heads * HEAD_DIM or x.stride(-1) != 1:
+        raise ValueError(f"{name} must be [B, L, {heads * HEAD_DIM}] with contiguous channels, got "
+                         f"{tuple(x.shape)} / strides {x.stride()}")
+
+
+def _require_norm_rope(weight, heads, rope):
+    if weight.dtype != torch.bfloat16 or tuple(weight.shape) != (heads * HEAD_DIM,) or not weight.is_contiguous():
+        raise ValueError(f"norm weight must be contiguous bf16 ({heads * HEAD_DIM},), got {weight.dtype} "
+                         f"{tuple(weight.shape)}")
+    t = rope.table
+    if t.dtype != torch.float64 or t.dim() != 3 or tuple(t.shape[1:]) != (HEAD_DIM // 2, 2) or not t.is_contiguous():
+        raise ValueError(f"rope table must be contiguous float64 [rows, {HEAD_DIM // 2}, 2], got {tuple(t.shape)}")
+    if t.device != weight.device:
+        raise ValueError("the rope table and the norm weight must be on the projection's device")
+
+
+def norm_rope_quant_q(q, heads, weight, eps, rope, ring=None, layer=0, seg_slots=(), want_roped=False):
+    """The q projection [B, Lq, heads * 128] bf16 -> RMSNorm (weight, eps) -> rotary embedding (`rope`: a
+    ChunkRope) -> (q8, q_scale, bias or None, roped bf16 [B, Lq, H, 128] or None), the quantised Q in the layouts
+    of quant_q."""
+    lib = _lib.load()
+    _require_rows("q", q, heads)
+    _require_norm_rope(weight, heads, rope)
+    b, lq = q.shape[0], q.shape[1]
+    bh, lp = b * heads, pad_to(lq, Q_TILE)
+    q8 = torch.empty(bh, lp, HEAD_DIM, dtype=torch.int8, device=q.device)
+    qs = torch.empty(bh, lp // Q_GROUP, dtype=torch.float32, device=q.device)
+    n_seg = len(seg_slots)
+    bias, km_ptr, slots, seg_arr = None, None, 1, None
+    if n_seg > 1:
+        bias = torch.empty(n_seg, bh, lp, dtype=torch.float32, device=q.device)
+        km_ptr, slots = _ptr(ring.km[layer]), ring.slots
+        seg_arr = (ctypes_i32 * n_seg)(*seg_slots)
+    roped = torch.empty(b, lq, heads, HEAD_DIM, dtype=torch.bfloat16, device=q.device) if want_roped else None
+    os_ = roped.stride()[:3] if roped is not None else (0, 0, 0)
+    st = lib.lbw_norm_rope_quant_q(_ptr(q), b, lq, heads, q.stride(0), q.stride(1), _ptr(weight), float(eps),
+                                   _ptr(rope.table), rope.table.shape[0], rope.grid_h, rope.grid_w, rope.start_frame,
+                                   _ptr(q8), _ptr(qs), km_ptr, slots, n_seg, seg_arr, _ptr(bias), _ptr(roped),
+                                   *os_, _stream(q))
+    _lib.check(st, "lbw_norm_rope_quant_q")
+    return q8, qs, bias, roped
+
+
+def norm_rope_kv_requant(k, v, heads, weight, eps, rope, ring, slot, layer=0, k_out=None, workspace=None):
+    """The k projection [B, L, heads * 128] bf16 -> RMSNorm -> rotary embedding -> roped bf16 K (into `k_out`,
+    [B, L, H, 128], allocated when None), and slot `slot` of `layer` of `ring` re-quantised from it and v
+    [B, L, H, 128] exactly as kv_requant would. Returns k_out."""
+    lib = _lib.load()
+    _require_rows("k", k, heads)
+    _require_norm_rope(weight, heads, rope)
+    _require_cuda_bf16("v", v)
+    b, n = k.shape[0], k.shape[1]
+    if tuple(v.shape) != (b, n, heads, HEAD_DIM):
+        raise ValueError(f"v {tuple(v.shape)} does not match k {tuple(k.shape)}")
+    if b != ring.batch or heads != ring.heads or n > ring.cap or not 0 <= layer < ring.layers:
+        raise ValueError(f"chunk of {n} tokens does not fit the ring (batch {ring.batch}, heads {ring.heads}, "
+                         f"cap {ring.cap}, layers {ring.layers})")
+    if k_out is None:
+        k_out = torch.empty(b, n, heads, HEAD_DIM, dtype=torch.bfloat16, device=k.device)
+    _require_cuda_bf16("k_out", k_out)
+    if tuple(k_out.shape) != (b, n, heads, HEAD_DIM):
+        raise ValueError(f"k_out {tuple(k_out.shape)} must be {(b, n, heads, HEAD_DIM)}")
+    if workspace is None:
+        workspace = requant_workspace(1, b * heads, n, k.device)
+    k8, ksc, km, v8, v8lo, vsc = ring.layer_view(layer)
+    vs, os_ = v.stride(), k_out.stride()
+    st = lib.lbw_norm_rope_kv_requant(_ptr(k), _ptr(v), b, n, heads, k.stride(0), k.stride(1), vs[0], vs[1], vs[2],
+                                      _ptr(weight), float(eps), _ptr(rope.table), rope.table.shape[0], rope.grid_h,
+                                      rope.grid_w, rope.start_frame, _ptr(k_out), os_[0], os_[1], os_[2], _ptr(k8),
+                                      _ptr(ksc), _ptr(km), _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap,
+                                      slot, _ptr(workspace), _stream(k))
+    _lib.check(st, "lbw_norm_rope_kv_requant")
+    return k_out
+
+
 _ATTN_WS = {}
 
 

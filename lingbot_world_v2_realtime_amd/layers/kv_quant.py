@@ -162,6 +162,18 @@ class QuantKVRing:
                            workspace=self._workspace(k.shape[0], n))
         self.lens[self.current] = n
 
+    def write_projected(self, layer, k, v, norm_weight, rope, eps=1e-6, k_out=None):
+        """write() from the k projection [B, L, H * 128] instead of the roped K: RMSNorm (norm_weight, eps) and
+        the rotary embedding (`rope`, a ChunkRope) are applied on the way in. Returns the roped bf16 K."""
+        n = k.shape[1]
+        if self.window_mode and self.current is None:
+            self._begin_chunk(n)
+        out = kernels.norm_rope_kv_requant(k, v, self.cache.heads, norm_weight, eps, rope, self.cache,
+                                           self.current, layer=layer, k_out=k_out,
+                                           workspace=self._workspace(1, n))
+        self.lens[self.current] = n
+        return out
+
     def attended_ranges(self):
         """(slot, first token, tokens) the attention reads, in order."""
         if not self.window_mode:
@@ -187,6 +199,18 @@ class QuantKVRing:
             raise RuntimeError("the current chunk has no K/V yet: call write() first")
         q8, qs, bias = kernels.quant_q(q, "NHD", self.cache, layer, slots)
         out = q.new_empty(q.shape)
+        return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale)
+
+    def attend_projected(self, q, layer, norm_weight, rope, eps=1e-6, sm_scale=None):
+        """attend() from the q projection [B, Lq, H * 128]: RMSNorm and the rotary embedding fused into the Q
+        quantisation. Returns [B, Lq, H, 128] bf16."""
+        b, lq = q.shape[0], q.shape[1]
+        h = self.cache.heads
+        slots, lens = self.attended()
+        if any(n == 0 for n in lens):
+            raise RuntimeError("the current chunk has no K/V yet: call write() first")
+        q8, qs, bias, _ = kernels.norm_rope_quant_q(q, h, norm_weight, eps, rope, self.cache, layer, slots)
+        out = q.new_empty(b, lq, h, kernels.HEAD_DIM)
         return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale)
 
     def commit(self):

@@ -30,7 +30,8 @@ Order of the K mean (fixed so it is reproducible bit for bit): token t of a chun
 b = t // 64 at row r = t % 64 = 4 q + j (q in 0..15, j in 0..3); blocks form super-blocks of 4 (u = b // 4).
 In fp32, every sum starting from +0 and running left to right:
   s[b, q]  = x[4q] + x[4q + 1] + x[4q + 2] + x[4q + 3]
-  B[b]     = s[b, 0] + s[b, 1] + ... + s[b, 15]
+  H[b, i]  = s[b, 8i] + s[b, 8i + 1] + ... + s[b, 8i + 7]   (the two 32-token halves, i = 0, 1)
+  B[b]     = H[b, 0] + H[b, 1]
   U[u]     = B[4u] + B[4u + 1] + B[4u + 2] + B[4u + 3]     (the blocks that exist)
   total    = U[0] + U[1] + ... + U[nsup - 1]
   mean     = total / n (fp32, correctly rounded), km = bf16(mean) round to nearest even.
@@ -132,9 +133,10 @@ def chunk_mean(k):
     s = torch.zeros(nb, 16, h, d, dtype=torch.float32)
     for j in range(4):
         s = s + x[:, :, j]
-    blk = torch.zeros(nb, h, d, dtype=torch.float32)
-    for q in range(16):
-        blk = blk + s[:, q]
+    half = torch.zeros(nb, 2, h, d, dtype=torch.float32)
+    for q in range(8):
+        half = half + s[:, q::8]
+    blk = half[:, 0] + half[:, 1]
     tot = torch.zeros(h, d, dtype=torch.float32)
     for u in range(0, nb, SUPER_BLOCK):
         sup = torch.zeros(h, d, dtype=torch.float32)

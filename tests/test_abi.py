@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declarations_are_bound_and_exported(lib):
     decl = declared_functions()
-    assert len(decl) == 11
+    assert len(decl) == 13
     assert set(decl) == set(_lib.SIGNATURES)
     for name, n in decl.items():
         assert len(_lib.SIGNATURES[name][1]) == n, name
@@ -62,8 +62,8 @@ def test_requant_workspace_formula(lib):
     for layers, bh, n in ((1, 1, 1), (30, 24, 1508), (2, 3, 64), (1, 5, 65), (30, 12, 6032), (1, 1, 262400)):
         nb = -(-n // 64)
         g = layers * bh
-        # per-block column sums and maxima, plus the per-channel V reciprocals
-        assert lib.lbw_kv_requant_workspace_bytes(layers, bh, n) == (2 * g * nb * 128 + g * 128) * 4
+        # column sums and maxima per 32-token half-block, plus the per-channel V reciprocals
+        assert lib.lbw_kv_requant_workspace_bytes(layers, bh, n) == (2 * g * 2 * nb * 128 + g * 128) * 4
     assert lib.lbw_kv_requant_workspace_bytes(0, 1, 1) == 0
 
 
@@ -107,6 +107,55 @@ def test_quant_q_argument_checks(lib):
     assert quant_q(lib, n_seg=2, seg=None) == E_NULL
     assert quant_q(lib, n_seg=2, seg=seg) == E_SEGMENTS   # slot 5 of a 4-slot cache
     assert quant_q(lib, n_seg=2, seg=seg, km=FAKE + 4) == E_ALIGN   # the K means are read as float4
+
+
+ROPE_ROWS = 1024
+
+
+def norm_rope_q(lib, **kw):
+    a = dict(q=FAKE, batch=1, lq=100, heads=2, st=(0, 256), w=FAKE, eps=1e-6, rope=FAKE, rows=ROPE_ROWS,
+             grid=(5, 4), f0=0, q8=FAKE, qs=FAKE, km=FAKE, slots=4, n_seg=0, seg=None, bias=FAKE, q_out=None,
+             os=(0, 256, 128))
+    a.update(kw)
+    return lib.lbw_norm_rope_quant_q(a["q"], a["batch"], a["lq"], a["heads"], *a["st"], a["w"], a["eps"], a["rope"],
+                                     a["rows"], *a["grid"], a["f0"], a["q8"], a["qs"], a["km"], a["slots"],
+                                     a["n_seg"], a["seg"], a["bias"], a["q_out"], *a["os"], None)
+
+
+def norm_rope_kv(lib, **kw):
+    a = dict(k=FAKE, v=FAKE, batch=1, len=100, heads=2, ks=(0, 256), vs=(0, 256, 128), w=FAKE, eps=1e-6,
+             rope=FAKE, rows=ROPE_ROWS, grid=(5, 4), f0=0, k_out=FAKE, os=(0, 256, 128), k8=FAKE, k_scale=FAKE,
+             km=FAKE, v8=FAKE, v8lo=None, v_scale=FAKE, slots=4, cap=128, slot=0, ws=FAKE)
+    a.update(kw)
+    return lib.lbw_norm_rope_kv_requant(a["k"], a["v"], a["batch"], a["len"], a["heads"], *a["ks"], *a["vs"], a["w"],
+                                        a["eps"], a["rope"], a["rows"], *a["grid"], a["f0"], a["k_out"], *a["os"],
+                                        a["k8"], a["k_scale"], a["km"], a["v8"], a["v8lo"], a["v_scale"],
+                                        a["slots"], a["cap"], a["slot"], a["ws"], None)
+
+
+def test_norm_rope_argument_checks(lib):
+    for call in (norm_rope_q, norm_rope_kv):
+        assert call(lib, w=None) == E_NULL
+        assert call(lib, rope=None) == E_NULL
+        assert call(lib, heads=17) == E_SHAPE                   # one wave per head, at most 16
+        assert call(lib, grid=(0, 4)) == E_SHAPE
+        assert call(lib, f0=-1) == E_SHAPE
+        assert call(lib, f0=ROPE_ROWS - 4) == E_SHAPE           # 100 tokens of 20-token frames need 5 frame rows
+        assert call(lib, grid=(ROPE_ROWS + 1, 1)) == E_SHAPE    # the height index would run past the table
+        assert call(lib, eps=float("nan")) == E_SHAPE
+        assert call(lib, rope=FAKE + 8) == E_ALIGN
+        assert call(lib, w=FAKE + 2) == E_ALIGN
+    assert norm_rope_q(lib, st=(0, 252)) == E_ALIGN
+    assert norm_rope_q(lib, q8=None) == E_NULL
+    assert norm_rope_q(lib, n_seg=9) == E_SEGMENTS
+    assert norm_rope_q(lib, n_seg=2, seg=(ctypes.c_int32 * 2)(0, 4)) == E_SEGMENTS
+    assert norm_rope_q(lib, q_out=FAKE, os=(0, 256, 12)) == E_ALIGN
+    assert norm_rope_kv(lib, k_out=None) == E_NULL
+    assert norm_rope_kv(lib, ws=None) == E_NULL
+    assert norm_rope_kv(lib, len=129) == E_SHAPE                # more tokens than the slot holds
+    assert norm_rope_kv(lib, slot=4) == E_SHAPE
+    assert norm_rope_kv(lib, vs=(0, 256, 12)) == E_ALIGN
+    assert norm_rope_kv(lib, k8=FAKE + 8) == E_ALIGN
 
 
 def attn(lib, **kw):
@@ -166,6 +215,8 @@ def test_valid_call_without_gfx950_is_refused(lib):
     assert requant(lib) == E_DEVICE
     assert quant_q(lib) == E_DEVICE
     assert attn(lib) == E_DEVICE
+    assert norm_rope_q(lib) == E_DEVICE
+    assert norm_rope_kv(lib) == E_DEVICE
     seg = (ctypes.c_int32 * 1)(0)
     ln = (ctypes.c_int32 * 1)(100)
     assert lib.lbw_attn_fwd_noalloc(FAKE, FAKE, None, 1, 100, 2, FAKE, FAKE, FAKE, None, FAKE, 1, 128, 1, seg, ln,
