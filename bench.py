@@ -11,6 +11,8 @@ Reported (one JSON line on stdout):
                lbw_attn_fwd): algorithmic ops per call / its HIP-event time vs 5.0 POPS dense INT8/FP8 MFMA
   requant      the K/V re-quant of a saved chunk for 30 layers in one call: algorithmic bytes (bf16 K, V read
                once; int8 K and one e4m3 V plane written once; scales) / time, vs 8 TB/s
+  prologue     the fused self-attention prologue per layer call (RMSNorm + RoPE of the q / k projections into
+               int8 Q and the current chunk's ring slot): algorithmic bytes / time, vs 8 TB/s
   chunk_sweep  the whole chunk captured in one HIP graph: 30 layers x 5 passes of the step above, then the
                30-layer re-quant that saves the chunk; seconds per chunk
   cpu_baseline the torch CPU emulation of the same scheme (oracle/emu.py) on a bounded sample of the call
@@ -79,6 +81,16 @@ def traffic_from_profiles():
         return json.load(f).get("call_hbm_bytes")
 
 
+def counters_from_profiles():
+    """MFMA counters of the attention kernel (rocprofv3 --pmc: SQ_INSTS_VALU_MFMA_MOPS_I8 / _F8 and
+    SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE), as committed in profiles/; None when not measured."""
+    p = os.path.join(ROOT, "profiles", "attn_fwd_cfg3_counters.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)
+
+
 def cpu_baseline(heads=3, q_rows=LQ):
     """The torch emulation on a sample: `heads` of the 12 heads, the first `q_rows` queries, all 24128 keys
     (4 chunks), including the Q quantisation and the current chunk's re-quant; scaled to the full call."""
@@ -125,6 +137,14 @@ def profile_only(args, dev):
         b = torch.empty_like(a)
         fn = lambda: b.copy_(a)                             # noqa: E731
         nbytes = 2 * a.numel() * a.element_size()
+    elif args.only == "prologue":
+        ring = QuantKVRing(1, 1, H, CHUNK, slots=MEM + 1, device=dev)
+        for _ in range(MEM):
+            mk = torch.randn(1, CHUNK, H, D, device=dev).to(torch.bfloat16)
+            ring.write(0, mk, mk)
+            ring.commit()
+        print(json.dumps({"only": "prologue", "result": prologue_call(dev, ring, args.steps)}), flush=True)
+        return
     elif args.only == "requant":
         kl = torch.randn(LAYERS, 1, CHUNK, H, D, device=dev).to(torch.bfloat16)
         vl = torch.randn(LAYERS, 1, CHUNK, H, D, device=dev).to(torch.bfloat16)
@@ -197,6 +217,49 @@ def chunk_sweep(dev, layers=LAYERS, passes=5, replays=3):
             "attention_TOPS": round(calls * attention_ops(LQ, LK) / sec / 1e12, 1), "hip_graph": True}
 
 
+def prologue_bytes(n=CHUNK, h=H, d=D, n_seg=MEM + 1):
+    """Algorithmic bytes of the fused prologue of one layer call: the q and k projections and V read once; the
+    int8 Q, int8 K and one e4m3 V plane written once, with their scales, the K mean and the per-chunk logit bias.
+    (The roped bf16 K this build writes and the quantiser reads back, and the residual V plane, are overhead.)"""
+    lp = (n + 255) // 256 * 256
+    nb = (n + 63) // 64
+    return 3 * n * h * d * 2 + 3 * n * h * d + h * (lp // 32) * 4 + n_seg * h * lp * 4 + nb * h * 4 + 2 * h * d * 4
+
+
+def prologue_call(dev, ring, steps=50):
+    """The self-attention prologue fused into the quantisation, per layer call at the chunk shape: RMSNorm +
+    RoPE of the q projection into int8 Q (+ the 4-chunk logit bias), and of the k projection into the roped K
+    and the current chunk's ring slot (lbw_norm_rope_quant_q + lbw_norm_rope_kv_requant), on `ring`'s layer 0."""
+    import torch
+    from lingbot_world_v2_realtime_amd import kernels
+    from lingbot_world_v2_realtime_amd.layers.prologue import ChunkRope, rope_freqs
+    g = torch.Generator(device=dev).manual_seed(3)
+    ql, kl = (torch.randn(1, CHUNK, H * D, device=dev, generator=g).to(torch.bfloat16) for _ in range(2))
+    v = torch.randn(1, CHUNK, H, D, device=dev, generator=g).to(torch.bfloat16)
+    wq, wk = (1 + 0.3 * torch.randn(H * D, device=dev, generator=g)).to(torch.bfloat16), \
+        (1 + 0.3 * torch.randn(H * D, device=dev, generator=g)).to(torch.bfloat16)
+    rope = ChunkRope.for_chunk(rope_freqs(dev), (4, 29, 52), current_start=3 * CHUNK)
+    k_out = torch.empty(1, CHUNK, H, D, device=dev, dtype=torch.bfloat16)
+    slots, _ = ring.attended()
+    stream = torch.cuda.current_stream(dev)
+
+    def kpart():
+        ring.write_projected(0, kl, v, wk, rope, k_out=k_out)
+
+    def qpart():
+        kernels.norm_rope_quant_q(ql, H, wq, 1e-6, rope, ring.cache, 0, slots)
+
+    for _ in range(5):
+        kpart(), qpart()
+    torch.cuda.synchronize()
+    k_ms = _timed(kpart, steps, stream)
+    q_ms = _timed(qpart, steps, stream)
+    nbytes = prologue_bytes()
+    ms = k_ms + q_ms
+    return {"ms": round(ms, 4), "q_ms": round(q_ms, 4), "kv_ms": round(k_ms, 4), "algorithmic_bytes": nbytes,
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def dropin_call(dev, lk=27144, calls=20):
     """The drop-in `attention()` call the reference ships (LINGBOT_ATTN=sage: sageattn over the bf16 window,
     lingbot/layers/attention.py:31-36): q [1,6032,12,128] against the reference's default 27144-key window, the
@@ -224,7 +287,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU emulation baseline")
     ap.add_argument("--cpu-heads", type=int, default=3)
     ap.add_argument("--no-sweep", action="store_true", help="skip the graph-captured per-chunk sweep")
-    ap.add_argument("--only", choices=["attn", "requant", "copy"],
+    ap.add_argument("--only", choices=["attn", "requant", "prologue", "copy"],
                     help="profiling run: after the set-up, launch only this part --steps times and print its "
                          "mean time (copy: a 2 GiB device-to-device copy, the byte-counter calibration)")
     args = ap.parse_args()
@@ -313,6 +376,15 @@ def main():
                     "GB/s": round(rq_gbps, 1), "frac_hbm": round(rq_gbps / HBM_PEAK_GBPS, 4),
                     "bytes_moved_two_v_planes": rq_moved},
     }
+    ctr = counters_from_profiles()
+    if ctr is not None:   # issued MFMA work from the counters, over this run's HIP-event time
+        issued = ctr["issued_ops"]
+        res["roofline"]["counters"] = {
+            "issued_ops_per_launch": issued, "issued_over_algorithmic": round(issued / ops, 4),
+            "issued_TOPS": round(issued / (attn_ms * 1e-3) / 1e12, 1),
+            "issued_frac": round(issued / (attn_ms * 1e-3) / 1e12 / MFMA_PEAK_TOPS, 4),
+            "mfma_busy": round(ctr["mfma_busy"], 4), "source": "profiles/attn_fwd_cfg3_counters.json"}
+    res["prologue"] = prologue_call(dev, ring)
     res["dropin_call"] = dropin_call(dev)
     res["chunk_sweep"] = None if args.no_sweep else chunk_sweep(dev)
     if not args.no_cpu:
