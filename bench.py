@@ -13,6 +13,8 @@ Reported (one JSON line on stdout):
                once; int8 K and one e4m3 V plane written once; scales) / time, vs 8 TB/s
   prologue     the fused self-attention prologue per layer call (RMSNorm + RoPE of the q / k projections into
                int8 Q and the current chunk's ring slot): algorithmic bytes / time, vs 8 TB/s
+  cross_attention  the DiT's cross-attention per layer call (6032 queries x 512 context tokens, bf16 MFMA):
+               algorithmic flops / time, vs 2.5 PFLOP/s dense bf16
   chunk_sweep  the whole chunk captured in one HIP graph: 30 layers x 5 passes of the step above, then the
                30-layer re-quant that saves the chunk; seconds per chunk
   cpu_baseline the torch CPU emulation of the same scheme (oracle/emu.py) on a bounded sample of the call
@@ -145,6 +147,9 @@ def profile_only(args, dev):
             ring.commit()
         print(json.dumps({"only": "prologue", "result": prologue_call(dev, ring, args.steps)}), flush=True)
         return
+    elif args.only == "cross":
+        print(json.dumps({"only": "cross", "result": cross_attention_call(dev, args.steps)}), flush=True)
+        return
     elif args.only == "requant":
         kl = torch.randn(LAYERS, 1, CHUNK, H, D, device=dev).to(torch.bfloat16)
         vl = torch.randn(LAYERS, 1, CHUNK, H, D, device=dev).to(torch.bfloat16)
@@ -260,6 +265,31 @@ def prologue_call(dev, ring, steps=50):
             "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+CONTEXT = 512               # text context tokens of the cross-attention
+
+
+def cross_attention_call(dev, steps=50):
+    """The DiT's cross-attention per layer call: Q [1,6032,12,128] bf16 against the 512-token text context
+    (prepared once per generation), bf16 flash attention on the MFMA with fp32 accumulation (lbw_cross_attn_fwd).
+    Algorithmic flops 4 * H * Lq * Lk * d against the dense bf16 peak."""
+    import torch
+    from lingbot_world_v2_realtime_amd import kernels
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = torch.randn(1, LQ, H, D, device=dev, generator=g).to(torch.bfloat16)
+    k, v = (torch.randn(1, CONTEXT, H, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(2))
+    ctx = kernels.CrossContext(k, v)
+    out = torch.empty_like(q)
+    for _ in range(5):
+        kernels.cross_attn_fwd(q, ctx, out)
+    torch.cuda.synchronize()
+    ms = _timed(lambda: kernels.cross_attn_fwd(q, ctx, out), steps, torch.cuda.current_stream(dev))
+    flops = attention_ops(LQ, CONTEXT)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"lq": LQ, "lk": CONTEXT, "ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+            "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "flops": flops}
+
+
 def dropin_call(dev, lk=27144, calls=20):
     """The drop-in `attention()` call the reference ships (LINGBOT_ATTN=sage: sageattn over the bf16 window,
     lingbot/layers/attention.py:31-36): q [1,6032,12,128] against the reference's default 27144-key window, the
@@ -287,7 +317,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU emulation baseline")
     ap.add_argument("--cpu-heads", type=int, default=3)
     ap.add_argument("--no-sweep", action="store_true", help="skip the graph-captured per-chunk sweep")
-    ap.add_argument("--only", choices=["attn", "requant", "prologue", "copy"],
+    ap.add_argument("--only", choices=["attn", "requant", "prologue", "cross", "copy"],
                     help="profiling run: after the set-up, launch only this part --steps times and print its "
                          "mean time (copy: a 2 GiB device-to-device copy, the byte-counter calibration)")
     args = ap.parse_args()
@@ -385,6 +415,7 @@ def main():
             "issued_frac": round(issued / (attn_ms * 1e-3) / 1e12 / MFMA_PEAK_TOPS, 4),
             "mfma_busy": round(ctr["mfma_busy"], 4), "source": "profiles/attn_fwd_cfg3_counters.json"}
     res["prologue"] = prologue_call(dev, ring)
+    res["cross_attention"] = cross_attention_call(dev)
     res["dropin_call"] = dropin_call(dev)
     res["chunk_sweep"] = None if args.no_sweep else chunk_sweep(dev)
     if not args.no_cpu:

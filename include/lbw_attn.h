@@ -130,6 +130,31 @@ int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, int64_t batch
                              void* stream);
 
 /*
+ * The cross-attention context in the layout lbw_cross_attn_fwd reads: k, v [batch][lk][heads][128] bf16 (strides
+ * *_s_batch, *_s_tok, *_s_head) -> k_prep [batch * heads][Lkp][128] and vt_prep [batch * heads][128][Lkp] (V
+ * transposed), Lkp = ceil64(lk), padding keys zero. The reference computes the cross-attention K / V once per
+ * generation and keeps them (crossattn_cache, lingbot/models/lingbot_world/transformer.py:251-266); this is the
+ * one-time step that goes with it.
+ */
+int lbw_cross_prepare(const uint16_t* k, const uint16_t* v, int64_t batch, int64_t lk, int64_t heads,
+                      int64_t k_s_batch, int64_t k_s_tok, int64_t k_s_head,
+                      int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
+                      uint16_t* k_prep, uint16_t* vt_prep, void* stream);
+
+/*
+ * Cross-attention, bf16 in / bf16 out with fp32 accumulation: q [batch][lq][heads][128] (strides q_s_*) against a
+ * context prepared by lbw_cross_prepare (lk keys), softmax(q k^T * sm_scale) v into out (strides o_s_*). k_lens:
+ * null, or a host array of `batch` key counts (1 .. lk) -- the varlen key lengths of the reference's flash call.
+ * batch <= 64. Replaces flash_attention(q, k, v, k_lens) of the cross-attention (transformer.py:272; the paper's
+ * FlashAttention, reference/wan/modules/attention.py:23-129).
+ */
+int lbw_cross_attn_fwd(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
+                       int64_t q_s_batch, int64_t q_s_tok, int64_t q_s_head,
+                       const uint16_t* k_prep, const uint16_t* vt_prep, int64_t lk, const int32_t* k_lens,
+                       uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
+                       float sm_scale, void* stream);
+
+/*
  * Quantized attention of Q (from lbw_quant_q) over the chunks seg_slot[0..n_seg) of one layer's cache
  * (pointers already offset to that layer), chunk c holding seg_len[c] valid tokens (1..cap). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the

@@ -1,0 +1,278 @@
+// Cross-attention of the DiT blocks against the text context (gfx950): bf16 flash attention with fp32
+// accumulation, for a short key sequence (the 512 context tokens) that every layer and pass re-reads.
+//
+//   cross_prepare_kernel: the context's K and V, [B, Lk, H, 128] bf16, into the layout the attention reads:
+//                         K [BH][Lkp][128] and V transposed, [BH][128][Lkp], keys zero-padded to Lkp = ceil64(Lk).
+//                         Done once per generation (the reference caches the cross-attention K / V the same way).
+//   cross_attn_kernel:    one workgroup per (128-query tile, batch * head), 4 waves x 32 queries. Per 64-key
+//                         tile (double-buffered in LDS): S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (lane = query,
+//                         16 keys per lane), an online softmax in the exp2 domain, P^T in bf16 straight from the
+//                         S^T registers into the B operand of O^T += V^T P^T (the keys of the two products are
+//                         permuted alike, so P needs no exchange between lanes), then O / l.
+#include "lbw_common.h"
+
+namespace lbw {
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+constexpr int XQ = 128;            // queries per workgroup
+constexpr int XK = 64;             // keys per tile
+constexpr int XWAVES = 4;
+constexpr int XT = XWAVES * 64;    // threads
+constexpr int K_ROW = D * 2 + 16;  // LDS bytes per K row (padded against bank conflicts)
+constexpr int VT_ROW = XK * 2 + 16;   // LDS bytes per V^T row (one channel, 64 keys)
+constexpr int K_TILE = XK * K_ROW;
+constexpr int VT_TILE = D * VT_ROW;
+constexpr int X_STAGE = K_TILE + VT_TILE;
+constexpr int XMAX_BATCH = 64;
+
+struct XArgs {
+  int64_t lq, lk, lkp, heads, bh;
+  int64_t q_sb, q_st, q_sh;
+  int64_t o_sb, o_st, o_sh;
+  float sl2;   // sm_scale * log2(e)
+  int klen[XMAX_BATCH];   // valid keys per batch entry (1 .. lk)
+};
+
+// Workgroup (64-key tile, batch * head): K rows copied, V transposed through LDS; keys past lk are zero.
+__global__ __launch_bounds__(256) void cross_prepare_kernel(const uint16_t* __restrict__ k,
+                                                            const uint16_t* __restrict__ v, int64_t lk,
+                                                            int64_t lkp, int64_t heads, int64_t k_sb,
+                                                            int64_t k_st, int64_t k_sh, int64_t v_sb,
+                                                            int64_t v_st, int64_t v_sh, uint16_t* __restrict__ kp,
+                                                            uint16_t* __restrict__ vt) {
+  __shared__ uint16_t s_v[XK][D + 2];
+  const int tile = blockIdx.x, bh = blockIdx.y, t = threadIdx.x;
+  const int64_t b = bh / heads, h = bh % heads;
+  // thread t: key 4 (t >> 4) .. + 3, channels 8 (t & 15) .. + 7
+  const int c8 = (t & 15) * 8;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int kk = 4 * (t >> 4) + j;
+    const int64_t key = (int64_t)tile * XK + kk;
+    v4i kw = {0, 0, 0, 0}, vw = {0, 0, 0, 0};
+    if (key < lk) {
+      kw = *(const v4i*)(k + b * k_sb + key * k_st + h * k_sh + c8);
+      vw = *(const v4i*)(v + b * v_sb + key * v_st + h * v_sh + c8);
+    }
+    *(v4i*)(kp + ((int64_t)bh * lkp + key) * D + c8) = kw;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      s_v[kk][c8 + 2 * q] = (uint16_t)((uint32_t)vw[q] & 0xFFFFu);
+      s_v[kk][c8 + 2 * q + 1] = (uint16_t)((uint32_t)vw[q] >> 16);
+    }
+  }
+  __syncthreads();
+  // thread t: channel t >> 1, keys 32 (t & 1) .. + 31 -> 64 contiguous bytes of V^T
+  const int ch = t >> 1, k0 = (t & 1) * 32;
+  uint32_t w[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) w[i] = (uint32_t)s_v[k0 + 2 * i][ch] | ((uint32_t)s_v[k0 + 2 * i + 1][ch] << 16);
+  uint16_t* dst = vt + ((int64_t)bh * D + ch) * lkp + (int64_t)tile * XK + k0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    *(v4i*)(dst + 8 * i) = v4i{(int)w[4 * i], (int)w[4 * i + 1], (int)w[4 * i + 2], (int)w[4 * i + 3]};
+}
+
+__device__ __forceinline__ bf8 as_bf8(const v4i x) { return __builtin_bit_cast(bf8, x); }
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+}
+
+__global__ __launch_bounds__(XT) void cross_attn_kernel(const uint16_t* __restrict__ q,
+                                                        const uint16_t* __restrict__ kp,
+                                                        const uint16_t* __restrict__ vt, XArgs a,
+                                                        uint16_t* __restrict__ out) {
+  __shared__ __align__(16) uint8_t xlds[2 * X_STAGE];
+  const int qt = blockIdx.x, bh = blockIdx.y;
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63, lq = lane & 31, hf = lane >> 5;
+  const int64_t b = bh / a.heads, h = bh % a.heads;
+  const int64_t q0 = (int64_t)qt * XQ + 32 * w;
+  const int64_t qrow = q0 + lq;
+  const int klen = a.klen[b];
+  const int ntile = (klen + XK - 1) / XK;
+  const uint16_t* kbase = kp + (int64_t)bh * a.lkp * D;
+  const uint16_t* vbase = vt + (int64_t)bh * D * a.lkp;
+
+  // Q^T B operand: lane (lq, hf) holds query qrow, channels 16 s + 8 hf .. + 8 (rows past lq are zero)
+  bf8 qf[8];
+  {
+    const uint16_t* qp = q + b * a.q_sb + qrow * a.q_st + h * a.q_sh + 8 * hf;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = as_bf8(qrow < a.lq ? *(const v4i*)(qp + 16 * s) : v4i{0, 0, 0, 0});
+  }
+
+  // tile loads: thread t moves 4 x 16 B of K (rows 16 i + (t >> 4), bytes 16 (t & 15)) and 4 x 16 B of V^T
+  // (channel 32 i + (t >> 3), keys 8 (t & 7) .. + 7)
+  v4i kreg[4], vreg[4];
+  auto load_tile = [&](int tl) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kreg[i] = *(const v4i*)(kbase + ((int64_t)tl * XK + 16 * i + (t >> 4)) * D + 8 * (t & 15));
+      vreg[i] = *(const v4i*)(vbase + (int64_t)(32 * i + (t >> 3)) * a.lkp + (int64_t)tl * XK + 8 * (t & 7));
+    }
+  };
+  auto store_tile = [&](int stg) {
+    uint8_t* sk = xlds + stg * X_STAGE;
+    uint8_t* sv = sk + K_TILE;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(v4i*)(sk + (16 * i + (t >> 4)) * K_ROW + 16 * (t & 15)) = kreg[i];
+      *(v4i*)(sv + (32 * i + (t >> 3)) * VT_ROW + 16 * (t & 7)) = vreg[i];
+    }
+  };
+
+  v16f o[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[mt][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int tl = 0; tl < ntile; ++tl) {
+    const int stg = tl & 1;
+    if (tl + 1 < ntile) load_tile(tl + 1);
+    const uint8_t* sk = xlds + stg * X_STAGE;
+    const uint8_t* sv = sk + K_TILE;
+    // S^T of keys 32 kt .. + 31 of the tile: lane (lq, hf) value i is key 32 kt + 8 (i >> 2) + 4 hf + (i & 3)
+    v16f s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      v16f acc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+      const uint8_t* kr = sk + (32 * kt + lq) * K_ROW + 16 * hf;
+#pragma unroll
+      for (int st = 0; st < 8; ++st)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(*(const v4i*)(kr + 32 * st)), qf[st], acc, 0, 0, 0);
+      s[kt] = acc;
+    }
+    // mask keys past klen, scale into the exp2 domain, online max
+    const int kbase_t = tl * XK + 4 * hf;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = kbase_t + 32 * kt + 8 * (i >> 2) + (i & 3);
+        const float x = key < klen ? s[kt][i] * a.sl2 : -INFINITY;
+        s[kt][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);   // finite: every tile holds at least one valid key
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    l_run *= alpha;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[mt][i] *= alpha;
+    // P^T fragments: (kt, u) = keys 32 kt + 16 u + {4 hf + 0..3, 8 + 4 hf + 0..3} = values i = 8 u .. 8 u + 7
+    v4i pf[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          p[j] = exp2f(s[kt][8 * u + j] - m_new);
+          l_run += p[j];
+        }
+        pf[kt][u] = v4i{(int)pack_bf16(p[0], p[1]), (int)pack_bf16(p[2], p[3]), (int)pack_bf16(p[4], p[5]),
+                        (int)pack_bf16(p[6], p[7])};
+      }
+    // O^T += V^T P^T: A = V^T rows 32 mt + lq, the same 8 keys per (kt, u) as the lane's P^T values
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      const uint8_t* vr = sv + (32 * mt + lq) * VT_ROW + 8 * hf;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const uint2 lo = *(const uint2*)(vr + 2 * (32 * kt + 16 * u));
+          const uint2 hi = *(const uint2*)(vr + 2 * (32 * kt + 16 * u + 8));
+          const v4i vf = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+          o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), as_bf8(pf[kt][u]), o[mt], 0, 0, 0);
+        }
+    }
+    if (tl + 1 < ntile) {
+      store_tile(stg ^ 1);   // the other stage: every wave finished reading it before the last barrier
+      __syncthreads();
+    }
+  }
+  l_run += __shfl_xor(l_run, 32);
+  if (qrow >= a.lq) return;
+  const float inv_l = 1.f / l_run;
+  uint16_t* op = out + b * a.o_sb + qrow * a.o_st + h * a.o_sh;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {   // channels 32 mt + 8 i + 4 hf + 0..3
+      const int ch = 32 * mt + 8 * i + 4 * hf;
+      *(uint2*)(op + ch) = make_uint2(pack_bf16(o[mt][4 * i] * inv_l, o[mt][4 * i + 1] * inv_l),
+                                      pack_bf16(o[mt][4 * i + 2] * inv_l, o[mt][4 * i + 3] * inv_l));
+    }
+}
+
+}  // namespace lbw
+
+using namespace lbw;
+
+extern "C" int lbw_cross_prepare(const uint16_t* k, const uint16_t* v, int64_t batch, int64_t lk, int64_t heads,
+                                 int64_t k_s_batch, int64_t k_s_tok, int64_t k_s_head, int64_t v_s_batch,
+                                 int64_t v_s_tok, int64_t v_s_head, uint16_t* k_prep, uint16_t* vt_prep,
+                                 void* stream) {
+  if (!k || !v || !k_prep || !vt_prep) return LBW_E_NULL;
+  if (batch <= 0 || lk <= 0 || heads <= 0 || batch * heads > 65535 || lk > (1 << 20)) return LBW_E_SHAPE;
+  const int64_t strides[6] = {k_s_batch, k_s_tok, k_s_head, v_s_batch, v_s_tok, v_s_head};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return LBW_E_ALIGN;
+  if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_prep | (uintptr_t)vt_prep) & 15) return LBW_E_ALIGN;
+  if (const int dv = check_device()) return dv;
+  const int64_t lkp = (lk + XK - 1) / XK * XK;
+  hipLaunchKernelGGL(cross_prepare_kernel, dim3((unsigned)(lkp / XK), (unsigned)(batch * heads)), dim3(256), 0,
+                     (hipStream_t)stream, k, v, lk, lkp, heads, k_s_batch, k_s_tok, k_s_head, v_s_batch, v_s_tok,
+                     v_s_head, k_prep, vt_prep);
+  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
+  return LBW_OK;
+}
+
+extern "C" int lbw_cross_attn_fwd(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads, int64_t q_s_batch,
+                                  int64_t q_s_tok, int64_t q_s_head, const uint16_t* k_prep,
+                                  const uint16_t* vt_prep, int64_t lk, const int32_t* k_lens, uint16_t* out,
+                                  int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head, float sm_scale,
+                                  void* stream) {
+  if (!q || !k_prep || !vt_prep || !out) return LBW_E_NULL;
+  if (batch <= 0 || lq <= 0 || heads <= 0 || lk <= 0 || batch > XMAX_BATCH || batch * heads > 65535 ||
+      lk > (1 << 20))
+    return LBW_E_SHAPE;
+  if (!(sm_scale > 0.f) || !(sm_scale < INFINITY)) return LBW_E_SHAPE;
+  const int64_t strides[6] = {q_s_batch, q_s_tok, q_s_head, o_s_batch, o_s_tok, o_s_head};
+  for (int64_t s : strides)
+    if (s % 8 != 0) return LBW_E_ALIGN;
+  if (((uintptr_t)q | (uintptr_t)k_prep | (uintptr_t)vt_prep | (uintptr_t)out) & 15) return LBW_E_ALIGN;
+  XArgs a;
+  a.lq = lq; a.lk = lk; a.lkp = (lk + XK - 1) / XK * XK; a.heads = heads; a.bh = batch * heads;
+  a.q_sb = q_s_batch; a.q_st = q_s_tok; a.q_sh = q_s_head;
+  a.o_sb = o_s_batch; a.o_st = o_s_tok; a.o_sh = o_s_head;
+  a.sl2 = sm_scale * 1.4426950408889634f;
+  for (int i = 0; i < XMAX_BATCH; ++i) a.klen[i] = (int)lk;
+  if (k_lens) {   // the varlen key lengths of the reference's flash call, a host array; each 1 .. lk
+    for (int i = 0; i < batch; ++i) {
+      if (k_lens[i] < 1 || k_lens[i] > lk) return LBW_E_SHAPE;
+      a.klen[i] = k_lens[i];
+    }
+  }
+  if ((lq + XQ - 1) / XQ > 0x7fffffff) return LBW_E_SHAPE;
+  if (const int dv = check_device()) return dv;
+  hipLaunchKernelGGL(cross_attn_kernel, dim3((unsigned)((lq + XQ - 1) / XQ), (unsigned)(batch * heads)), dim3(XT),
+                     0, (hipStream_t)stream, q, k_prep, vt_prep, a, out);
+  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
+  return LBW_OK;
+}

@@ -210,6 +210,54 @@ def norm_rope_kv_requant(k, v, heads, weight, eps, rope, ring, slot, layer=0, k_
     return k_out
 
 
+class CrossContext:
+    """One layer's cross-attention context in the kernel's layout: K [BH, Lkp, 128] and V^T [BH, 128, Lkp] bf16
+    (Lkp = ceil64(Lk), padding zero), made once from k, v [B, Lk, H, 128] (lbw_cross_prepare)."""
+
+    def __init__(self, k, v):
+        lib = _lib.load()
+        _require_cuda_bf16("k", k)
+        _require_cuda_bf16("v", v)
+        if k.dim() != 4 or tuple(v.shape) != tuple(k.shape):
+            raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must be the same [B, Lk, H, 128]")
+        b, lk, h, _ = k.shape
+        lkp = pad_to(lk, K_BLOCK)
+        self.batch, self.lk, self.heads = b, lk, h
+        self.k = torch.empty(b * h, lkp, HEAD_DIM, dtype=torch.bfloat16, device=k.device)
+        self.vt = torch.empty(b * h, HEAD_DIM, lkp, dtype=torch.bfloat16, device=k.device)
+        ks, vs = k.stride(), v.stride()
+        st = lib.lbw_cross_prepare(_ptr(k), _ptr(v), b, lk, h, ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
+                                   _ptr(self.k), _ptr(self.vt), _stream(k))
+        _lib.check(st, "lbw_cross_prepare")
+
+
+def cross_attn_fwd(q, ctx, out=None, sm_scale=None, k_lens=None):
+    """Cross-attention of q [B, Lq, H, 128] bf16 against a CrossContext; k_lens: None or B key counts (host
+    ints). Returns out [B, Lq, H, 128] bf16."""
+    lib = _lib.load()
+    _require_cuda_bf16("q", q)
+    b, lq, h, _ = q.shape
+    if (b, h) != (ctx.batch, ctx.heads):
+        raise ValueError(f"q {tuple(q.shape)} does not match the context (batch {ctx.batch}, heads {ctx.heads})")
+    if out is None:
+        out = torch.empty_like(q)
+    _require_cuda_bf16("out", out)
+    if tuple(out.shape) != tuple(q.shape):
+        raise ValueError(f"out {tuple(out.shape)} must be {tuple(q.shape)}")
+    lens = None
+    if k_lens is not None:
+        vals = [int(x) for x in (k_lens.tolist() if hasattr(k_lens, "tolist") else k_lens)]
+        if len(vals) != b:
+            raise ValueError(f"k_lens needs {b} entries, got {len(vals)}")
+        lens = (ctypes_i32 * b)(*vals)
+    sm_scale = HEAD_DIM ** -0.5 if sm_scale is None else float(sm_scale)
+    qs, os_ = q.stride(), out.stride()
+    st = lib.lbw_cross_attn_fwd(_ptr(q), b, lq, h, qs[0], qs[1], qs[2], _ptr(ctx.k), _ptr(ctx.vt), ctx.lk, lens,
+                                _ptr(out), os_[0], os_[1], os_[2], sm_scale, _stream(q))
+    _lib.check(st, "lbw_cross_attn_fwd")
+    return out
+
+
 _ATTN_WS = {}
 
 

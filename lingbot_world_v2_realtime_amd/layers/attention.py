@@ -3,8 +3,9 @@
 Mirrors lingbot/layers/attention.py:1-40. `LINGBOT_ATTN=sage` (read at import time, as the reference does
 at :22-24) routes the plain batched self-attention call -- no q_lens / k_lens, no dropout, non-causal, the
 only way the causal DiT calls it -- through `sage_attention`: INT8 QK^T and FP8 PV in HIP kernels on gfx950.
-Everything else goes to the paper's attention semantics (reference/wan/modules/attention.py:132-178), served
-here by PyTorch SDPA because flash_attn has no ROCm wheel in this stack.
+The cross-attention's `flash_attention` runs a bf16 flash-attention HIP kernel (lbw_cross_attn_fwd); everything
+else goes to the paper's attention semantics (reference/wan/modules/attention.py:132-178), served here by PyTorch
+SDPA because flash_attn has no ROCm wheel in this stack.
 """
 import os
 import warnings
@@ -13,7 +14,7 @@ import torch
 
 from .. import kernels
 
-__all__ = ["attention", "flash_attention", "sage_attention"]
+__all__ = ["attention", "flash_attention", "sage_attention", "CrossAttnCache", "cross_attention"]
 
 _QUANT = os.environ.get("LINGBOT_ATTN") in ("sage", "sage_kvq")
 
@@ -75,9 +76,57 @@ def _paper_attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_sc
     return out.transpose(1, 2).contiguous()
 
 
+_FLASH_DEFAULTS = {"q_lens": None, "dropout_p": 0., "q_scale": None, "causal": False, "window_size": (-1, -1)}
+
+
 def flash_attention(q, k, v, k_lens=None, **kw):
-    """The paper's FlashAttention call (lingbot/layers/attention.py:16-20); SDPA on this stack."""
-    return _paper_attention(q, k, v, k_lens=k_lens, **kw)
+    """The paper's FlashAttention call (lingbot/layers/attention.py:16-20 -> reference/wan/modules/attention.py:
+    23-129) as the DiT's cross-attention makes it: q [B, Lq, H, 128], k / v [B, Lk, H, 128] on the GPU, optional
+    per-batch key counts k_lens; bf16 attention with fp32 accumulation in a HIP kernel (lbw_cross_attn_fwd), out in
+    q.dtype. Inputs that are not fp16 / bf16 are cast to `dtype` first, as the reference does; the kernel computes
+    in bf16. Calls with arguments the kernel does not take (q_lens, dropout, causal, a window, q_scale) get the
+    paper's SDPA form instead."""
+    opts = {key: kw.get(key, dflt) for key, dflt in _FLASH_DEFAULTS.items()}
+    dtype = kw.get("dtype", torch.bfloat16)
+    if any(opts[key] != dflt for key, dflt in _FLASH_DEFAULTS.items() if key != "window_size") or \
+            tuple(opts["window_size"]) != (-1, -1) or q.shape[-1] != kernels.HEAD_DIM:
+        return _paper_attention(q, k, v, k_lens=k_lens, **kw)
+    out_dtype = q.dtype
+
+    def half(x):
+        return x if x.dtype in (torch.float16, torch.bfloat16) else x.to(dtype)
+
+    qh, kh, vh = (half(x).to(torch.bfloat16) for x in (q, k, v))
+    ctx = kernels.CrossContext(kh, vh)
+    out = kernels.cross_attn_fwd(qh, ctx, sm_scale=kw.get("softmax_scale"), k_lens=k_lens)
+    return out.to(out_dtype)
+
+
+class CrossAttnCache:
+    """One layer's cross-attention K / V kept across the forwards of a generation, in the kernel's layout (the
+    reference's crossattn_cache, lingbot/models/lingbot_world/transformer.py:251-266: filled on the first call,
+    read by every later one)."""
+
+    def __init__(self):
+        self.ctx = None
+
+    @property
+    def is_init(self):
+        return self.ctx is not None
+
+    def fill(self, k, v):
+        """k, v [B, Lk, H, 128] bf16: the normed context keys and values."""
+        self.ctx = kernels.CrossContext(k, v)
+
+    def reset(self):
+        self.ctx = None
+
+
+def cross_attention(q, cache, k_lens=None, softmax_scale=None):
+    """q [B, Lq, H, 128] bf16 against the filled CrossAttnCache -> [B, Lq, H, 128] bf16."""
+    if cache.ctx is None:
+        raise RuntimeError("the cross-attention cache is empty: fill() it with the context's K / V first")
+    return kernels.cross_attn_fwd(q, cache.ctx, sm_scale=softmax_scale, k_lens=k_lens)
 
 
 def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=None, q_scale=None,

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declarations_are_bound_and_exported(lib):
     decl = declared_functions()
-    assert len(decl) == 13
+    assert len(decl) == 15
     assert set(decl) == set(_lib.SIGNATURES)
     for name, n in decl.items():
         assert len(_lib.SIGNATURES[name][1]) == n, name
@@ -158,6 +158,32 @@ def test_norm_rope_argument_checks(lib):
     assert norm_rope_kv(lib, k8=FAKE + 8) == E_ALIGN
 
 
+def cross(lib, **kw):
+    a = dict(q=FAKE, batch=1, lq=100, heads=2, qs=(0, 256, 128), kp=FAKE, vt=FAKE, lk=512, lens=None, out=FAKE,
+             os=(0, 256, 128), sm=0.088)
+    a.update(kw)
+    return lib.lbw_cross_attn_fwd(a["q"], a["batch"], a["lq"], a["heads"], *a["qs"], a["kp"], a["vt"], a["lk"],
+                                  a["lens"], a["out"], *a["os"], a["sm"], None)
+
+
+def test_cross_attention_argument_checks(lib):
+    assert cross(lib, q=None) == E_NULL
+    assert cross(lib, vt=None) == E_NULL
+    assert cross(lib, lk=0) == E_SHAPE
+    assert cross(lib, batch=65) == E_SHAPE                     # per-batch key counts travel in the arguments
+    assert cross(lib, sm=0.0) == E_SHAPE
+    assert cross(lib, sm=float("inf")) == E_SHAPE
+    assert cross(lib, lens=(ctypes.c_int32 * 1)(0)) == E_SHAPE  # each count 1 .. lk
+    assert cross(lib, lens=(ctypes.c_int32 * 1)(513)) == E_SHAPE
+    assert cross(lib, qs=(0, 256, 12)) == E_ALIGN
+    assert cross(lib, out=FAKE + 4) == E_ALIGN
+    prep = lambda **kw: lib.lbw_cross_prepare(kw.get("k", FAKE), FAKE, 1, kw.get("lk", 512), 2,  # noqa: E731
+                                              0, 256, kw.get("ksh", 128), 0, 256, 128, FAKE, FAKE, None)
+    assert prep(k=None) == E_NULL
+    assert prep(lk=0) == E_SHAPE
+    assert prep(ksh=130) == E_ALIGN
+
+
 def attn(lib, **kw):
     seg = (ctypes.c_int32 * 8)(0, 1, 2, 3, 0, 0, 0, 0)
     ln = (ctypes.c_int32 * 8)(128, 128, 128, 100, 0, 0, 0, 0)
@@ -217,6 +243,8 @@ def test_valid_call_without_gfx950_is_refused(lib):
     assert attn(lib) == E_DEVICE
     assert norm_rope_q(lib) == E_DEVICE
     assert norm_rope_kv(lib) == E_DEVICE
+    assert cross(lib) == E_DEVICE
+    assert lib.lbw_cross_prepare(FAKE, FAKE, 1, 512, 2, 0, 256, 128, 0, 256, 128, FAKE, FAKE, None) == E_DEVICE
     seg = (ctypes.c_int32 * 1)(0)
     ln = (ctypes.c_int32 * 1)(100)
     assert lib.lbw_attn_fwd_noalloc(FAKE, FAKE, None, 1, 100, 2, FAKE, FAKE, FAKE, None, FAKE, 1, 128, 1, seg, ln,
