@@ -15,6 +15,8 @@ Reported (one JSON line on stdout):
                int8 Q and the current chunk's ring slot): algorithmic bytes / time, vs 8 TB/s
   cross_attention  the DiT's cross-attention per layer call (6032 queries x 512 context tokens, bf16 MFMA):
                algorithmic flops / time, vs 2.5 PFLOP/s dense bf16
+  fp8_linear   the DiT's FP8 linears at 6032 tokens (rowwise e4m3 activation quant + hipBLASLt FP8 GEMM):
+               flops / time, vs 5.0 PFLOP/s dense fp8
   chunk_sweep  the whole chunk captured in one HIP graph: 30 layers x 5 passes of the step above, then the
                30-layer re-quant that saves the chunk; seconds per chunk
   cpu_baseline the torch CPU emulation of the same scheme (oracle/emu.py) on a bounded sample of the call
@@ -290,6 +292,36 @@ def cross_attention_call(dev, steps=50):
             "frac_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "flops": flops}
 
 
+FP8_PEAK_TFLOPS = 5000.0    # MI355X dense fp8 MFMA
+DIM, FFN = 1536, 8960       # the DiT's model and feed-forward widths
+
+
+def fp8_linear_calls(dev, steps=30):
+    """The DiT's FP8 linears at the chunk shape (6032 tokens): q/k/v/o (1536 -> 1536) and the two feed-forward
+    layers (1536 -> 8960, 8960 -> 1536). Per call: the activation quantisation (lbw_quant_rows_fp8) and
+    hipBLASLt's rowwise-scaled FP8 GEMM with the bias. Flops 2 M K N against 5.0 PFLOP/s dense fp8."""
+    import torch
+    from lingbot_world_v2_realtime_amd import kernels
+    from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear
+    out = {}
+    stream = torch.cuda.current_stream(dev)
+    for name, (k, n) in (("proj_1536x1536", (DIM, DIM)), ("ffn_up_1536x8960", (DIM, FFN)),
+                         ("ffn_down_8960x1536", (FFN, DIM))):
+        lin = torch.nn.Linear(k, n).to(torch.bfloat16).to(dev)
+        f = FP8Linear(lin)
+        x = torch.randn(1, LQ, k, device=dev).to(torch.bfloat16)
+        for _ in range(3):
+            f(x)
+        torch.cuda.synchronize()
+        ms = _timed(lambda: f(x), steps, stream)
+        q_ms = _timed(lambda: kernels.quant_rows_fp8(x.view(LQ, k)), steps, stream)
+        flops = 2.0 * LQ * k * n
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 4), "act_quant_ms": round(q_ms, 4), "TFLOP/s": round(tf, 1),
+                     "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+    return out
+
+
 def dropin_call(dev, lk=27144, calls=20):
     """The drop-in `attention()` call the reference ships (LINGBOT_ATTN=sage: sageattn over the bf16 window,
     lingbot/layers/attention.py:31-36): q [1,6032,12,128] against the reference's default 27144-key window, the
@@ -416,6 +448,7 @@ def main():
             "mfma_busy": round(ctr["mfma_busy"], 4), "source": "profiles/attn_fwd_cfg3_counters.json"}
     res["prologue"] = prologue_call(dev, ring)
     res["cross_attention"] = cross_attention_call(dev)
+    res["fp8_linear"] = fp8_linear_calls(dev)
     res["dropin_call"] = dropin_call(dev)
     res["chunk_sweep"] = None if args.no_sweep else chunk_sweep(dev)
     if not args.no_cpu:

@@ -155,6 +155,15 @@ int lbw_cross_attn_fwd(const uint16_t* q, int64_t batch, int64_t lq, int64_t hea
                        float sm_scale, void* stream);
 
 /*
+ * Rowwise FP8 quantisation of x [rows][cols] (bf16, or fp32 when x_is_fp32; row stride s_row elements, cols a
+ * multiple of 16): scale[row] = max(amax(|x[row]|) / 448, 1e-12) and x8[row][col] = e4m3(x / scale), round to
+ * nearest even, rows packed (cols bytes apart). The quantisation of lingbot/layers/linear.py:15-26 (FP8Linear):
+ * once per output row for a weight, per token for the activations of every call.
+ */
+int lbw_quant_rows_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t cols, int64_t s_row,
+                       uint8_t* x8, float* scale, void* stream);
+
+/*
  * Quantized attention of Q (from lbw_quant_q) over the chunks seg_slot[0..n_seg) of one layer's cache
  * (pointers already offset to that layer), chunk c holding seg_len[c] valid tokens (1..cap). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the

@@ -6,7 +6,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 LIB = os.path.join(HERE, "liblbw_attn.so")
-SOURCES = ["lbw_abi.hip", "kv_requant.hip", "quant_q.hip", "prologue.hip", "cross_attn.hip", "attn_fwd.hip"]
+SOURCES = ["lbw_abi.hip", "kv_requant.hip", "quant_q.hip", "prologue.hip", "cross_attn.hip", "fp8_quant.hip", "attn_fwd.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",

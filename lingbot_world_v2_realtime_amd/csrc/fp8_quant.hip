@@ -1,0 +1,87 @@
+// Rowwise FP8 quantisation for the FP8 linear layers (gfx950): per row, scale = max(amax / 448, 1e-12) and
+// e4m3(x / scale) with round-to-nearest-even, the scheme of the reference's FP8Linear for its weights (once, per
+// output row) and its activations (every call, per token). The GEMM itself is a plain rowwise-scaled FP8 GEMM
+// (hipBLASLt); this kernel is the part around it that runs on every call.
+//
+// One workgroup per row: 256 threads, 16-byte loads; the amax pass and the quantise pass read the row twice (the
+// second read comes from the cache: a row is a few KB).
+#include "lbw_common.h"
+
+namespace lbw {
+
+constexpr float FP8_MAX = 448.f;
+constexpr float FP8_SCALE_FLOOR = 1e-12f;
+
+template <typename T>
+struct Row8;
+
+template <>
+struct Row8<uint16_t> {   // bf16: 8 values = 16 bytes
+  static __device__ __forceinline__ void load(const uint16_t* p, float* f) { unpack8(*(const v4i*)p, f); }
+};
+
+template <>
+struct Row8<float> {      // fp32: 8 values = 32 bytes
+  static __device__ __forceinline__ void load(const float* p, float* f) {
+    const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict__ x, int64_t cols, int64_t s_row,
+                                                             uint8_t* __restrict__ x8, float* __restrict__ scale) {
+  __shared__ float s_red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * s_row;
+  const int t = threadIdx.x;
+  float amax = 0.f;
+  for (int64_t c = 8 * (int64_t)t; c < cols; c += 8 * 256) {
+    float f[8];
+    Row8<T>::load(xr + c, f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+  }
+  amax = wave_max(amax);
+  if ((t & 63) == 0) s_red[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float sc = fmaxf(__fdiv_rn(amax, FP8_MAX), FP8_SCALE_FLOOR);
+  if (t == 0) scale[row] = sc;
+  uint8_t* outr = x8 + row * cols;
+  for (int64_t c = 8 * (int64_t)t; c < cols; c += 8 * 256) {
+    float f[8];
+    Row8<T>::load(xr + c, f);
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      // x / scale is within 448 up to its own rounding; the clamp keeps a rounding above 448 off the overflow path
+      const float y0 = fminf(fmaxf(__fdiv_rn(f[e], sc), -FP8_MAX), FP8_MAX);
+      const float y1 = fminf(fmaxf(__fdiv_rn(f[e + 1], sc), -FP8_MAX), FP8_MAX);
+      const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false) & 0xFFFFu;
+      w[e >> 2] |= pk << (16 * ((e >> 1) & 1));
+    }
+    *(uint2*)(outr + c) = make_uint2(w[0], w[1]);
+  }
+}
+
+}  // namespace lbw
+
+using namespace lbw;
+
+extern "C" int lbw_quant_rows_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t cols, int64_t s_row,
+                                  uint8_t* x8, float* scale, void* stream) {
+  if (!x || !x8 || !scale) return LBW_E_NULL;
+  if (rows <= 0 || cols <= 0 || rows > 0x7fffffff || cols % 16 != 0) return LBW_E_SHAPE;
+  if (s_row < cols) return LBW_E_SHAPE;
+  if (s_row % 8 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)x8 & 7)) return LBW_E_ALIGN;
+  if (const int dv = check_device()) return dv;
+  if (x_is_fp32)
+    hipLaunchKernelGGL(quant_rows_fp8_kernel<float>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)x, cols, s_row, x8, scale);
+  else
+    hipLaunchKernelGGL(quant_rows_fp8_kernel<uint16_t>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, cols, s_row, x8, scale);
+  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
+  return LBW_OK;
+}

@@ -258,6 +258,25 @@ def cross_attn_fwd(q, ctx, out=None, sm_scale=None, k_lens=None):
     return out
 
 
+def quant_rows_fp8(x):
+    """Rowwise e4m3 of a 2-d bf16 / fp32 device tensor x [rows, cols] (cols a multiple of 16, unit column stride):
+    (x8 float8_e4m3fn [rows, cols], scale fp32 [rows, 1]) with x ~ x8 * scale."""
+    lib = _lib.load()
+    if not x.is_cuda:
+        raise ValueError("x must be a device tensor (the FP8 path has no CPU implementation)")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be bfloat16 or float32, got {x.dtype}")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError(f"x must be 2-d with contiguous rows, got {tuple(x.shape)} / {x.stride()}")
+    rows, cols = x.shape
+    x8 = torch.empty(rows, cols, dtype=torch.float8_e4m3fn, device=x.device)
+    scale = torch.empty(rows, 1, dtype=torch.float32, device=x.device)
+    st = lib.lbw_quant_rows_fp8(_ptr(x), int(x.dtype == torch.float32), rows, cols, x.stride(0), _ptr(x8),
+                                _ptr(scale), _stream(x))
+    _lib.check(st, "lbw_quant_rows_fp8")
+    return x8, scale
+
+
 _ATTN_WS = {}
 
 

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declarations_are_bound_and_exported(lib):
     decl = declared_functions()
-    assert len(decl) == 15
+    assert len(decl) == 16
     assert set(decl) == set(_lib.SIGNATURES)
     for name, n in decl.items():
         assert len(_lib.SIGNATURES[name][1]) == n, name
@@ -182,6 +182,19 @@ def test_cross_attention_argument_checks(lib):
     assert prep(k=None) == E_NULL
     assert prep(lk=0) == E_SHAPE
     assert prep(ksh=130) == E_ALIGN
+
+
+def test_quant_rows_fp8_argument_checks(lib):
+    q = lambda **kw: lib.lbw_quant_rows_fp8(kw.get("x", FAKE), 0, kw.get("rows", 10), kw.get("cols", 256),  # noqa: E731
+                                            kw.get("s", 256), kw.get("x8", FAKE), FAKE, None)
+    assert q(x=None) == E_NULL
+    assert q(rows=0) == E_SHAPE
+    assert q(cols=100) == E_SHAPE          # multiples of 16, as the reference converts
+    assert q(s=128) == E_SHAPE             # rows would overlap
+    assert q(s=260) == E_ALIGN
+    assert q(x=FAKE + 8) == E_ALIGN
+    if hip_device_count() == 0:
+        assert q() == E_DEVICE
 
 
 def attn(lib, **kw):

@@ -1,0 +1,86 @@
+"""The FP8 linear path on the device: the rowwise e4m3 quantisation kernel (lbw_quant_rows_fp8, through the
+C-ABI) bit for bit against the oracle, and FP8Linear (that kernel + hipBLASLt's rowwise-scaled FP8 GEMM) against
+the fp32 product of the same quantised operands."""
+import pytest
+import torch
+
+from conftest import record
+from oracle import fp8
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _k():
+    from lingbot_world_v2_realtime_amd import kernels
+    return kernels
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(1, 16, torch.bfloat16), (37, 1536, torch.bfloat16),
+                                             (6032, 1536, torch.bfloat16), (100, 8960, torch.bfloat16),
+                                             (1536, 1536, torch.float32), (3, 2064, torch.float32)])
+def test_quant_rows_bit_exact(rows, cols, dtype):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * torch.exp(torch.randn(rows, 1, generator=g) * 2)).to(dtype)
+    x[0, :] = 0                                            # the scale floor
+    x8, sc = _k().quant_rows_fp8(x.to(DEV))
+    torch.cuda.synchronize()
+    rb, rs = fp8.quant_rows(x)
+    assert torch.equal(x8.view(torch.uint8).cpu(), rb)
+    assert torch.equal(sc.cpu(), rs)
+
+
+def test_quant_rows_strided_view():
+    x = torch.randn(50, 2 * 256, dtype=torch.bfloat16)
+    view = x[:, :256]                                      # row stride 512
+    x8, sc = _k().quant_rows_fp8(x.to(DEV)[:, :256])
+    torch.cuda.synchronize()
+    rb, rs = fp8.quant_rows(view)
+    assert torch.equal(x8.view(torch.uint8).cpu(), rb) and torch.equal(sc.cpu(), rs)
+
+
+@pytest.mark.parametrize("m,k,n,bias", [(6032, 1536, 1536, True), (333, 1536, 8960, False), (64, 8960, 1536, True)])
+def test_fp8_linear(m, k, n, bias):
+    from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear
+    g = torch.Generator().manual_seed(m)
+    lin = torch.nn.Linear(k, n, bias=bias).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(n, k, generator=g) * 0.02)
+        if bias:
+            lin.bias.copy_(torch.randn(n, generator=g) * 0.1)
+    lin = lin.to(DEV)
+    f = FP8Linear(lin)
+    # a 3-d activation [2, m / 2, k] when m is even (the DiT's [B, L, C]), else 2-d
+    shape = (2, m // 2, k) if m % 2 == 0 else (m, k)
+    x = torch.randn(*shape, generator=g).to(torch.bfloat16)
+    y = f(x.to(DEV))
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16 and y.shape == (*x.shape[:-1], n)
+    # the same quantised operands in fp32 on the CPU
+    xb, xs = fp8.quant_rows(x.reshape(-1, k))
+    wb, ws = fp8.quant_rows(lin.weight.detach().cpu())
+    ref = fp8.dequant_rows(xb, xs) @ fp8.dequant_rows(wb, ws).t()
+    if bias:
+        ref = ref + lin.bias.detach().cpu().to(torch.bfloat16).float()
+    e = (y.reshape(-1, n).float().cpu() - ref).abs()
+    scale = ref.abs().max().item()
+    assert e.max().item() <= 1e-2 * scale, (e.max().item(), scale)   # bf16 output + fp32 accumulation order
+    # and against the bf16 linear it replaces: the fp8 rounding of both operands
+    full = (x.reshape(-1, k).float() @ lin.weight.detach().cpu().float().t())
+    if bias:
+        full = full + lin.bias.detach().cpu().float()
+    rel = ((y.reshape(-1, n).float().cpu() - full).norm() / full.norm()).item()
+    record(f"FP8Linear {m}x{k}x{n}: vs same-operand fp32 max {e.max().item():.2e} (|ref| max {scale:.2e}); "
+           f"vs bf16 linear rel-L2 {rel:.2e}")
+    assert rel < 6e-2
+
+
+def test_convert_to_fp8_selection():
+    from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear, convert_to_fp8
+    blk = torch.nn.Sequential(torch.nn.Linear(1536, 1536), torch.nn.Sequential(torch.nn.Linear(1536, 8960)),
+                              torch.nn.Linear(256, 1536), torch.nn.Linear(1536, 1000)).to(torch.bfloat16).to(DEV)
+    n_fp8, n_all = convert_to_fp8(blk)
+    assert (n_fp8, n_all) == (2, 4)
+    assert isinstance(blk[0], FP8Linear) and isinstance(blk[1][0], FP8Linear)
+    assert isinstance(blk[2], torch.nn.Linear) and isinstance(blk[3], torch.nn.Linear)
