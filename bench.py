@@ -116,6 +116,53 @@ def cpu_baseline(heads=3, q_rows=LQ):
                       f"current-chunk quant), {dt:.2f} s, scaled x{1 / frac:.0f} -> {full_s:.1f} s per call"}
 
 
+def config_table(dev, ms_cfg3, rq_ms, sweep_s, cpu3, heads_cpu=3):
+    """The per-config GPU / CPU table: cfg 1 (1508 x 1508) and cfg 2 (6032 x 6032) attention calls on the GPU (one
+    chunk, HIP events) and in the CPU emulation (all 12 heads for cfg 1; `heads_cpu` heads scaled for cfg 2); cfg 3
+    from the main measurement; cfg 4 (one layer's re-quant) on both; cfg 5 from the graph sweep, its CPU figure
+    composed from the measured cfg 3 and cfg 4 CPU times (150 calls + 30 layers)."""
+    import torch
+    from oracle import emu
+    from lingbot_world_v2_realtime_amd import sage_attention
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    out = {}
+    for name, n, hs in (("cfg1", 1508, H), ("cfg2", 6032, heads_cpu)):
+        q, k, v, _ = synthetic_inputs(n, n, h=H, seed=0)
+        qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+        for _ in range(3):
+            sage_attention(qd, kd, vd)
+        torch.cuda.synchronize()
+        g_ms = _timed(lambda: sage_attention(qd, kd, vd), 20, torch.cuda.current_stream(dev))
+        t0 = time.perf_counter()
+        chunk = emu.requant(k[:, :, :hs], v[:, :, :hs])
+        emu.attention(q[:, :, :hs], [chunk])
+        c_s = (time.perf_counter() - t0) * H / hs
+        ops = attention_ops(n, n)
+        out[name] = {"gpu_ms": round(g_ms, 4), "gpu_TOPS": round(ops / (g_ms * 1e-3) / 1e12, 1),
+                     "frac": round(ops / (g_ms * 1e-3) / 1e12 / MFMA_PEAK_TOPS, 4), "cpu_s": round(c_s, 3),
+                     "cpu_TOPS": round(ops / c_s / 1e12, 5), "cpu_sample": f"{hs} of {H} heads"}
+    ops3 = attention_ops(LQ, LK)
+    cpu3_s = ops3 / (cpu3["value"] * 1e12) if cpu3 else None
+    out["cfg3"] = {"gpu_ms": round(ms_cfg3, 4), "gpu_TOPS": round(ops3 / (ms_cfg3 * 1e-3) / 1e12, 1),
+                   "frac": round(ops3 / (ms_cfg3 * 1e-3) / 1e12 / MFMA_PEAK_TOPS, 4),
+                   "cpu_s": None if cpu3_s is None else round(cpu3_s, 2),
+                   "cpu_TOPS": None if cpu3 is None else cpu3["value"]}
+    q, k, v, _ = synthetic_inputs(CHUNK, CHUNK, h=H, seed=2)
+    t0 = time.perf_counter()
+    emu.requant(k, v)
+    c4 = time.perf_counter() - t0
+    b4 = requant_bytes(CHUNK, H, D)
+    out["cfg4_layer"] = {"gpu_ms": round(rq_ms / LAYERS, 4), "gpu_GBps": round(b4 / (rq_ms / LAYERS * 1e-3) / 1e9, 1),
+                         "cpu_s": round(c4, 3), "cpu_GBps": round(b4 / c4 / 1e9, 3),
+                         "note": "GPU: the 30-layer call / 30"}
+    out["cfg5_chunk"] = {"gpu_s": sweep_s,
+                         "cpu_s": None if cpu3_s is None else round(150 * cpu3_s + LAYERS * c4, 1),
+                         "note": "CPU: 150 x the cfg 3 call + 30 x the cfg 4 layer, composed"}
+    out["cores"] = cores
+    return out
+
+
 def _timed(fn, n, stream):
     """Mean milliseconds of fn() over n launches, HIP events on `stream`."""
     import torch
@@ -349,6 +396,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU emulation baseline")
     ap.add_argument("--cpu-heads", type=int, default=3)
     ap.add_argument("--no-sweep", action="store_true", help="skip the graph-captured per-chunk sweep")
+    ap.add_argument("--table", action="store_true",
+                    help="add the per-config GPU / CPU table (cfg 1, cfg 2 attention; cfg 4 layer; cfg 5 composed)")
     ap.add_argument("--only", choices=["attn", "requant", "prologue", "cross", "copy"],
                     help="profiling run: after the set-up, launch only this part --steps times and print its "
                          "mean time (copy: a 2 GiB device-to-device copy, the byte-counter calibration)")
@@ -455,6 +504,10 @@ def main():
         res["cpu_baseline"] = cpu_baseline(args.cpu_heads)
     else:
         res["cpu_baseline"] = None
+    if args.table:
+        res["config_table"] = config_table(dev, attn_ms, rq_ms,
+                                           res["chunk_sweep"]["s_per_chunk"] if res["chunk_sweep"] else None,
+                                           res["cpu_baseline"], args.cpu_heads)
     print(json.dumps(res), flush=True)
 
 
