@@ -4,11 +4,13 @@
 //   cross_prepare_kernel: the context's K and V, [B, Lk, H, 128] bf16, into the layout the attention reads:
 //                         K [BH][Lkp][128] and V transposed, [BH][128][Lkp], keys zero-padded to Lkp = ceil64(Lk).
 //                         Done once per generation (the reference caches the cross-attention K / V the same way).
-//   cross_attn_kernel:    one workgroup per (128-query tile, batch * head), 4 waves x 32 queries. Per 64-key
-//                         tile (double-buffered in LDS): S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (lane = query,
-//                         16 keys per lane), an online softmax in the exp2 domain, P^T in bf16 straight from the
-//                         S^T registers into the B operand of O^T += V^T P^T (the keys of the two products are
-//                         permuted alike, so P needs no exchange between lanes), then O / l.
+//   cross_attn_kernel:    one workgroup per (128-query tile, batch * head), 4 waves x 32 queries, two workgroups a
+//                         CU. Per 64-key tile (two LDS stages, filled by direct global -> LDS loads one tile
+//                         ahead): S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (lane = query, 16 keys per lane), an
+//                         online softmax in the exp2 domain (one FMA and one exp2 per score, the key mask only on
+//                         a ragged last tile), P^T in bf16 straight from the S^T registers into the B operand of
+//                         O^T += V^T P^T (the keys of the two products are permuted alike, so P needs no exchange
+//                         between lanes), then O / l.
 #include "lbw_common.h"
 
 namespace lbw {
@@ -19,11 +21,6 @@ constexpr int XQ = 128;            // queries per workgroup
 constexpr int XK = 64;             // keys per tile
 constexpr int XWAVES = 4;
 constexpr int XT = XWAVES * 64;    // threads
-constexpr int K_ROW = D * 2 + 16;  // LDS bytes per K row (padded against bank conflicts)
-constexpr int VT_ROW = XK * 2 + 16;   // LDS bytes per V^T row (one channel, 64 keys)
-constexpr int K_TILE = XK * K_ROW;
-constexpr int VT_TILE = D * VT_ROW;
-constexpr int X_STAGE = K_TILE + VT_TILE;
 constexpr int XMAX_BATCH = 64;
 
 struct XArgs {
@@ -76,24 +73,45 @@ __global__ __launch_bounds__(256) void cross_prepare_kernel(const uint16_t* __re
 
 __device__ __forceinline__ bf8 as_bf8(const v4i x) { return __builtin_bit_cast(bf8, x); }
 
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+// two fp32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  const bf2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
-__global__ __launch_bounds__(XT) void cross_attn_kernel(const uint16_t* __restrict__ q,
-                                                        const uint16_t* __restrict__ kp,
-                                                        const uint16_t* __restrict__ vt, XArgs a,
-                                                        uint16_t* __restrict__ out) {
-  __shared__ __align__(16) uint8_t xlds[2 * X_STAGE];
+// Global -> LDS copy of 16 bytes per lane (lane i lands at M0 + 16 i), as inline asm: the compiler's builtin is
+// modelled as a FLAT access that may touch LDS, which would make every LDS wait drain all reads in flight.
+__device__ __forceinline__ void xdma16(const void* src, uint8_t* lds) {
+  uint32_t keep;
+  const uint32_t dst = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)lds;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+               "s_mov_b32 m0, %0"
+               : "=&s"(keep) : "v"(src), "s"(dst) : "memory");
+}
+
+// LDS tiles, XOR-swizzled by row so the fragment reads spread over the banks:
+//   K   [64 keys][256 B]: 16-byte chunk c of row r sits at position c ^ (r & 15)
+//   V^T [128 channels][128 B]: chunk c of row r sits at position c ^ ((r >> 1) & 7)
+constexpr int XK_TILE = XK * D * 2;          // 16 KB
+constexpr int XV_TILE = D * XK * 2;          // 16 KB
+constexpr int XSTAGE = XK_TILE + XV_TILE;
+
+__global__ __launch_bounds__(XT, 2) void cross_attn_kernel(const uint16_t* __restrict__ q,
+                                                           const uint16_t* __restrict__ kp,
+                                                           const uint16_t* __restrict__ vt, XArgs a,
+                                                           uint16_t* __restrict__ out) {
+  __shared__ __align__(16) uint8_t xlds[2 * XSTAGE];
   const int qt = blockIdx.x, bh = blockIdx.y;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, lq = lane & 31, hf = lane >> 5;
+  const int t = threadIdx.x, lane = t & 63, lq = lane & 31, hf = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t b = bh / a.heads, h = bh % a.heads;
-  const int64_t q0 = (int64_t)qt * XQ + 32 * w;
-  const int64_t qrow = q0 + lq;
+  const int64_t qrow = (int64_t)qt * XQ + 32 * w + lq;
   const int klen = a.klen[b];
   const int ntile = (klen + XK - 1) / XK;
-  const uint16_t* kbase = kp + (int64_t)bh * a.lkp * D;
-  const uint16_t* vbase = vt + (int64_t)bh * D * a.lkp;
+  const uint8_t* kbase = (const uint8_t*)(kp + (int64_t)bh * a.lkp * D);
+  const uint8_t* vbase = (const uint8_t*)(vt + (int64_t)bh * D * a.lkp);
+  const int64_t vrow_bytes = a.lkp * 2;
 
   // Q^T B operand: lane (lq, hf) holds query qrow, channels 16 s + 8 hf .. + 8 (rows past lq are zero)
   bf8 qf[8];
@@ -103,23 +121,17 @@ __global__ __launch_bounds__(XT) void cross_attn_kernel(const uint16_t* __restri
     for (int s = 0; s < 8; ++s) qf[s] = as_bf8(qrow < a.lq ? *(const v4i*)(qp + 16 * s) : v4i{0, 0, 0, 0});
   }
 
-  // tile loads: thread t moves 4 x 16 B of K (rows 16 i + (t >> 4), bytes 16 (t & 15)) and 4 x 16 B of V^T
-  // (channel 32 i + (t >> 3), keys 8 (t & 7) .. + 7)
-  v4i kreg[4], vreg[4];
-  auto load_tile = [&](int tl) {
+  // DMA: wave w moves K rows 16 w .. 16 w + 15 (4 x 1 KB) and V^T rows 32 w .. 32 w + 31 (4 x 1 KB) of a tile
+  auto issue = [&](int tl, int stg) {
+    uint8_t* sk = xlds + stg * XSTAGE;
+    uint8_t* sv = sk + XK_TILE;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      kreg[i] = *(const v4i*)(kbase + ((int64_t)tl * XK + 16 * i + (t >> 4)) * D + 8 * (t & 15));
-      vreg[i] = *(const v4i*)(vbase + (int64_t)(32 * i + (t >> 3)) * a.lkp + (int64_t)tl * XK + 8 * (t & 7));
-    }
-  };
-  auto store_tile = [&](int stg) {
-    uint8_t* sk = xlds + stg * X_STAGE;
-    uint8_t* sv = sk + K_TILE;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(v4i*)(sk + (16 * i + (t >> 4)) * K_ROW + 16 * (t & 15)) = kreg[i];
-      *(v4i*)(sv + (32 * i + (t >> 3)) * VT_ROW + 16 * (t & 7)) = vreg[i];
+      const int r = 16 * w + 4 * i + (lane >> 4), p = lane & 15;
+      xdma16(kbase + ((int64_t)tl * XK + r) * (D * 2) + ((p ^ (r & 15)) << 4), sk + (16 * w + 4 * i) * 256);
+      const int rv = 32 * w + 8 * i + (lane >> 3), pv = lane & 7;
+      xdma16(vbase + rv * vrow_bytes + (int64_t)tl * (XK * 2) + ((pv ^ ((rv >> 1) & 7)) << 4),
+             sv + (32 * w + 8 * i) * 128);
     }
   };
 
@@ -128,51 +140,58 @@ __global__ __launch_bounds__(XT) void cross_attn_kernel(const uint16_t* __restri
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) o[mt][i] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_ref = -INFINITY, l_run = 0.f;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
+  issue(0, 0);
   for (int tl = 0; tl < ntile; ++tl) {
     const int stg = tl & 1;
-    if (tl + 1 < ntile) load_tile(tl + 1);
-    const uint8_t* sk = xlds + stg * X_STAGE;
-    const uint8_t* sv = sk + K_TILE;
-    // S^T of keys 32 kt .. + 31 of the tile: lane (lq, hf) value i is key 32 kt + 8 (i >> 2) + 4 hf + (i & 3)
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's pieces of tile tl have landed
+    __syncthreads();                      // ... and every wave's; every wave is done with the other stage
+    if (tl + 1 < ntile) issue(tl + 1, stg ^ 1);
+    const uint8_t* sk = xlds + stg * XSTAGE;
+    const uint8_t* sv = sk + XK_TILE;
+    // S^T of keys 32 kt .. + 31: lane (lq, hf) value i is key 32 kt + 8 (i >> 2) + 4 hf + (i & 3)
     v16f s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       v16f acc;
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-      const uint8_t* kr = sk + (32 * kt + lq) * K_ROW + 16 * hf;
+      const int r = 32 * kt + lq;
+      const uint8_t* kr = sk + r * 256;
 #pragma unroll
       for (int st = 0; st < 8; ++st)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(*(const v4i*)(kr + 32 * st)), qf[st], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(*(const v4i*)(kr + (((2 * st + hf) ^ (r & 15)) << 4))),
+                                                      qf[st], acc, 0, 0, 0);
       s[kt] = acc;
     }
-    // mask keys past klen, scale into the exp2 domain, online max
-    const int kbase_t = tl * XK + 4 * hf;
+    if ((tl + 1) * XK > klen) {   // the ragged last tile: keys past klen drop out
+      const int kb = tl * XK + 4 * hf;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (kb + 32 * kt + 8 * (i >> 2) + (i & 3) >= klen) s[kt][i] = -INFINITY;
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int key = kbase_t + 32 * kt + 8 * (i >> 2) + (i & 3);
-        const float x = key < klen ? s[kt][i] * a.sl2 : -INFINITY;
-        s[kt][i] = x;
-        mx = fmaxf(mx, x);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);   // finite: every tile holds at least one valid key
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.sl2;   // exp2 domain; finite: every tile holds a valid key
+    // the exact running max: the row's largest P is exactly 1, which keeps its bf16 rounding error at zero (a
+    // reference max that moves only by steps measured 19 % more mean error on a peaked softmax)
+    const float m_new = fmaxf(m_ref, mx);
+    const float alpha = exp2f(m_ref - m_new);
     l_run *= alpha;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[mt][i] *= alpha;
-    // P^T fragments: (kt, u) = keys 32 kt + 16 u + {4 hf + 0..3, 8 + 4 hf + 0..3} = values i = 8 u .. 8 u + 7
+    m_ref = m_new;
+    // P^T fragments (kt, u): values i = 8 u .. 8 u + 7 = keys 32 kt + 16 u + {4 hf + 0..3, 8 + 4 hf + 0..3};
+    // P = exp2(s sl2 - m) <= 1
+    const float nm = -m_ref;
     v4i pf[2][2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -181,29 +200,27 @@ __global__ __launch_bounds__(XT) void cross_attn_kernel(const uint16_t* __restri
         float p[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          p[j] = exp2f(s[kt][8 * u + j] - m_new);
+          p[j] = exp2f(fmaf(s[kt][8 * u + j], a.sl2, nm));
           l_run += p[j];
         }
         pf[kt][u] = v4i{(int)pack_bf16(p[0], p[1]), (int)pack_bf16(p[2], p[3]), (int)pack_bf16(p[4], p[5]),
                         (int)pack_bf16(p[6], p[7])};
       }
-    // O^T += V^T P^T: A = V^T rows 32 mt + lq, the same 8 keys per (kt, u) as the lane's P^T values
+    // O^T += V^T P^T: A = V^T row 32 mt + lq, the lane's 8 keys of (kt, u) as two 8-byte pieces
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const uint8_t* vr = sv + (32 * mt + lq) * VT_ROW + 8 * hf;
+      const int r = 32 * mt + lq, sw = (r >> 1) & 7;
+      const uint8_t* vr = sv + r * 128 + 8 * hf;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const uint2 lo = *(const uint2*)(vr + 2 * (32 * kt + 16 * u));
-          const uint2 hi = *(const uint2*)(vr + 2 * (32 * kt + 16 * u + 8));
+          const int c = 4 * kt + 2 * u;   // 16-byte chunks c and c + 1 hold keys 32 kt + 16 u + 0..7 and + 8..15
+          const uint2 lo = *(const uint2*)(vr + ((c ^ sw) << 4));
+          const uint2 hi = *(const uint2*)(vr + (((c + 1) ^ sw) << 4));
           const v4i vf = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
           o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), as_bf8(pf[kt][u]), o[mt], 0, 0, 0);
         }
-    }
-    if (tl + 1 < ntile) {
-      store_tile(stg ^ 1);   // the other stage: every wave finished reading it before the last barrier
-      __syncthreads();
     }
   }
   l_run += __shfl_xor(l_run, 32);
