@@ -66,12 +66,12 @@ __device__ __forceinline__ uint32_t bf_pair(float lo, float hi) {
   return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
 }
 
-// The wave's rows of one projection (src already offset to the batch), normalised, weighted and roped in place,
-// kept as packed bf16: x[s][j][q] = channels 8 g + 2 q, 8 g + 2 q + 1 of row 4 (rq + 4 s) + j; rows past len are
-// 0. s_cs must be staged; the barriers here order it before its reads.
-__device__ __forceinline__ void norm_rope_rows(uint32_t (&x)[2][4][4], const uint16_t* __restrict__ src,
-                                               const uint16_t* __restrict__ w, const ProArgs& a, int64_t row0,
-                                               double* s_ss, float* s_r, const double2* s_cs) {
+// The wave's rows of one projection (src already offset to the batch), kept as packed bf16: x[s][j][q] = channels
+// 8 g + 2 q, 8 g + 2 q + 1 of row 4 (rq + 4 s) + j; rows past len are 0. Issued before the rope table is staged,
+// so the two sets of loads are in flight together. norm_rope_rows below needs s_cs staged; its barriers order
+// the staging before the reads.
+__device__ __forceinline__ void load_rows(uint32_t (&x)[2][4][4], const uint16_t* __restrict__ src,
+                                          const ProArgs& a, int64_t row0) {
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, rq = lane >> 4, g = lane & 15;
   const uint16_t* p = src + h * D + g * 8;
 #pragma unroll
@@ -83,6 +83,12 @@ __device__ __forceinline__ void norm_rope_rows(uint32_t (&x)[2][4][4], const uin
 #pragma unroll
       for (int q = 0; q < 4; ++q) x[s][j][q] = (uint32_t)v[q];
     }
+}
+
+// x (from load_rows) normalised, weighted and roped in place.
+__device__ __forceinline__ void norm_rope_rows(uint32_t (&x)[2][4][4], const uint16_t* __restrict__ w,
+                                               const ProArgs& a, double* s_ss, float* s_r, const double2* s_cs) {
+  const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, rq = lane >> 4, g = lane & 15;
   double ss[2][4];
 #pragma unroll
   for (int s = 0; s < 2; ++s)
@@ -155,9 +161,10 @@ __global__ __launch_bounds__(MAXT) void norm_rope_q_kernel(const uint16_t* __res
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, rq = lane >> 4, g = lane & 15;
   const int64_t row0 = (int64_t)grp * PR;
   const int64_t bh = (int64_t)b * a.heads + h;
-  stage_rope(s_cs, tab, a, row0);
   uint32_t x[2][4][4];
-  norm_rope_rows(x, q + b * a.x_sb, w, a, row0, s_ss, s_r, s_cs);
+  load_rows(x, q + b * a.x_sb, a, row0);
+  stage_rope(s_cs, tab, a, row0);
+  norm_rope_rows(x, w, a, s_ss, s_r, s_cs);
   float amax = 0.f;
 #pragma unroll
   for (int s = 0; s < 2; ++s)
@@ -223,9 +230,10 @@ __global__ __launch_bounds__(MAXT) void norm_rope_k_kernel(const uint16_t* __res
   const int half = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, rq = lane >> 4, g = lane & 15;
   const int64_t row0 = (int64_t)half * PR;
-  stage_rope(s_cs, tab, a, row0);
   uint32_t x[2][4][4];
-  norm_rope_rows(x, k + b * a.x_sb, w, a, row0, s_ss, s_r, s_cs);
+  load_rows(x, k + b * a.x_sb, a, row0);
+  stage_rope(s_cs, tab, a, row0);
+  norm_rope_rows(x, w, a, s_ss, s_r, s_cs);
   uint16_t* ko = k_out + b * a.o_sb + h * a.o_sh + g * 8;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
