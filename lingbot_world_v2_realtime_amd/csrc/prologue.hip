@@ -59,11 +59,14 @@ __device__ __forceinline__ void stage_rope(double2* s_cs, const double2* __restr
   }
 }
 
-// Two bf16 (low half first) <-> two fp32.
+// Two bf16 (low half first) <-> two fp32. The rounding is v_cvt_pk_bf16_f32 (round to nearest even, the same
+// bits as the integer rounding of the other kernels for every finite value), one instruction for two values.
+typedef __bf16 pbf2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
 __device__ __forceinline__ uint32_t bf_pair(float lo, float hi) {
-  return (uint32_t)f32_to_bf16_bits(lo) | ((uint32_t)f32_to_bf16_bits(hi) << 16);
+  const pbf2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // The wave's rows of one projection (src already offset to the batch), kept as packed bf16: x[s][j][q] = channels
@@ -133,8 +136,9 @@ __device__ __forceinline__ void norm_rope_rows(uint32_t (&x)[2][4][4], const uin
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint32_t u = x[s][j][q], wq = (uint32_t)wv[q];
-        const float n0 = bf16_round(bf16_round(bf_lo(u) * r) * bf_lo(wq));
-        const float n1 = bf16_round(bf16_round(bf_hi(u) * r) * bf_hi(wq));
+        const uint32_t y = bf_pair(bf_lo(u) * r, bf_hi(u) * r);                     // bf16(x r)
+        const uint32_t nn = bf_pair(bf_lo(y) * bf_lo(wq), bf_hi(y) * bf_hi(wq));    // bf16(y w)
+        const float n0 = bf_lo(nn), n1 = bf_hi(nn);
         const double2 c = cs[q];
         const double re = (double)n0 * c.x - (double)n1 * c.y;
         const double im = (double)n0 * c.y + (double)n1 * c.x;

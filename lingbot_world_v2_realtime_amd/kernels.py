@@ -35,6 +35,14 @@ def _require_cuda_bf16(name, t):
         raise ValueError(f"{name} must have a contiguous head dim of {HEAD_DIM}, got shape {tuple(t.shape)}")
 
 
+def _same_device(what, *tensors):
+    """Every tensor (None skipped) on one device: a kernel launched on the current device would otherwise read or
+    write another GPU's memory through a raw pointer."""
+    devs = {t.device for t in tensors if t is not None}
+    if len(devs) > 1:
+        raise ValueError(f"{what}: tensors on different devices {sorted(str(d) for d in devs)}")
+
+
 class RingCache:
     """Quantised K/V ring for `layers` layers x `slots` chunk slots of capacity `cap` tokens (a multiple of 64).
 
@@ -91,6 +99,7 @@ def kv_requant(k, v, ring, slot, layer0=0, workspace=None):
     _require_cuda_bf16("v", v)
     if k.shape != v.shape:
         raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+    _same_device("kv_requant", k, v, ring.k8, workspace)
     if k.dim() == 4:
         k, v = k.unsqueeze(0), v.unsqueeze(0)
     nl, b, n, h, _ = k.shape
@@ -113,6 +122,8 @@ def quant_q(q, layout="NHD", ring=None, layer=0, seg_slots=()):
     lib = _lib.load()
     _require_cuda_bf16("q", q)
     b, lq, h, s_b, s_t, s_h = _dims(q, layout)
+    if len(seg_slots) > 1:
+        _same_device("quant_q", q, ring.km)
     bh, lp = b * h, pad_to(lq, Q_TILE)
     q8 = torch.empty(bh, lp, HEAD_DIM, dtype=torch.int8, device=q.device)
     qs = torch.empty(bh, lp // Q_GROUP, dtype=torch.float32, device=q.device)
@@ -158,6 +169,7 @@ def norm_rope_quant_q(q, heads, weight, eps, rope, ring=None, layer=0, seg_slots
     lib = _lib.load()
     _require_rows("q", q, heads)
     _require_norm_rope(weight, heads, rope)
+    _same_device("norm_rope_quant_q", q, weight, rope.table, ring.km if len(seg_slots) > 1 else None)
     b, lq = q.shape[0], q.shape[1]
     bh, lp = b * heads, pad_to(lq, Q_TILE)
     q8 = torch.empty(bh, lp, HEAD_DIM, dtype=torch.int8, device=q.device)
@@ -195,6 +207,7 @@ def norm_rope_kv_requant(k, v, heads, weight, eps, rope, ring, slot, layer=0, k_
     if k_out is None:
         k_out = torch.empty(b, n, heads, HEAD_DIM, dtype=torch.bfloat16, device=k.device)
     _require_cuda_bf16("k_out", k_out)
+    _same_device("norm_rope_kv_requant", k, v, weight, rope.table, ring.k8, k_out, workspace)
     if tuple(k_out.shape) != (b, n, heads, HEAD_DIM):
         raise ValueError(f"k_out {tuple(k_out.shape)} must be {(b, n, heads, HEAD_DIM)}")
     if workspace is None:
@@ -220,6 +233,7 @@ class CrossContext:
         _require_cuda_bf16("v", v)
         if k.dim() != 4 or tuple(v.shape) != tuple(k.shape):
             raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must be the same [B, Lk, H, 128]")
+        _same_device("CrossContext", k, v)
         b, lk, h, _ = k.shape
         lkp = pad_to(lk, K_BLOCK)
         self.batch, self.lk, self.heads = b, lk, h
@@ -244,6 +258,7 @@ def cross_attn_fwd(q, ctx, out=None, sm_scale=None, k_lens=None):
     _require_cuda_bf16("out", out)
     if tuple(out.shape) != tuple(q.shape):
         raise ValueError(f"out {tuple(out.shape)} must be {tuple(q.shape)}")
+    _same_device("cross_attn_fwd", q, ctx.k, out)
     lens = None
     if k_lens is not None:
         vals = [int(x) for x in (k_lens.tolist() if hasattr(k_lens, "tolist") else k_lens)]
@@ -305,6 +320,7 @@ def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_le
     if not 1 <= n_seg <= MAX_SEGMENTS or len(seg_lens) != n_seg:
         raise ValueError(f"need 1..{MAX_SEGMENTS} chunks with a length each, got {seg_slots} / {seg_lens}")
     _require_cuda_bf16("out", out)
+    _same_device("attn_fwd", q8, q_scale, bias, out, ring.k8, workspace)
     ob, ol, oh, o_b, o_t, o_h = _dims(out, layout)
     if (ob, ol, oh) != (batch, lq, heads):   # the kernel writes every row of this shape through out's strides
         raise ValueError(f"out {tuple(out.shape)} ({layout}) does not hold batch {batch} x {lq} rows x {heads} heads")

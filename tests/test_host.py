@@ -158,3 +158,14 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_same_device_guard():
+    """Wrappers refuse tensors spread over devices (a raw pointer of another device would be dereferenced)."""
+    import torch
+    from lingbot_world_v2_realtime_amd import kernels
+    a = torch.zeros(2)
+    b = torch.zeros(2, device="meta")
+    kernels._same_device("x", a, None, a)
+    with pytest.raises(ValueError):
+        kernels._same_device("x", a, b)
