@@ -11,60 +11,78 @@ struct QArgs {
   int seg_slot[LBW_MAX_SEGMENTS];
 };
 
-// One wave per (32-row group, batch*head): lane = 2 * row + half, each lane owns 64 channels of one row.
-__global__ __launch_bounds__(64) void quant_q_kernel(const uint16_t* __restrict__ q, QArgs a,
-                                                     int8_t* __restrict__ q8, float* __restrict__ q_scale,
-                                                     const float* __restrict__ km, float* __restrict__ bias) {
-  __shared__ __align__(16) float s_km[LBW_MAX_SEGMENTS][D];   // the chunks' K means for the logit bias
-  const int grp = blockIdx.x, bh = blockIdx.y;
-  const int lane = threadIdx.x, r = lane >> 1, half = lane & 1;
-  const int64_t row = (int64_t)grp * QG + r;
+// One wave per (32-row group, batch*head), four waves (four batch*heads) per workgroup. Lane (rq, g) =
+// (lane >> 4, lane & 15) holds channels 8 g .. 8 g + 7 of rows 4 (rq + 4 s) + j, s = 0, 1, j = 0..3, so each
+// 16-byte load instruction reads 4 rows x 256 contiguous bytes. The logit bias of a row is its 16 lanes' 8-term
+// dot products with the chunk mean, summed pairwise (xor 1, 2, 4, 8).
+constexpr int QQ_WAVES = 4;
+__global__ __launch_bounds__(64 * QQ_WAVES) void quant_q_kernel(const uint16_t* __restrict__ q, QArgs a,
+                                                               int8_t* __restrict__ q8, float* __restrict__ q_scale,
+                                                               const float* __restrict__ km,
+                                                               float* __restrict__ bias) {
+  const int grp = blockIdx.x;
+  const int lane = threadIdx.x & 63, rq = lane >> 4, g = lane & 15;
+  const int64_t bh = (int64_t)blockIdx.y * QQ_WAVES + (threadIdx.x >> 6);
+  if (bh >= a.bh) return;   // wave-uniform; the kernel has no barrier
   const int64_t b = bh / a.heads, h = bh % a.heads;
-  const bool ok = row < a.lq;
-  const uint16_t* qp = q + b * a.sb + row * a.st + h * a.sh + half * 64;
-  // the K means go through LDS once per row group: read from global memory inside the dot products below,
-  // every lane would wait on 16 dependent loads per chunk
-  if (a.n_seg > 1) {
-    for (int i = lane; i < a.n_seg * (D / 4); i += 64) {
-      const int c = i / (D / 4), k4 = i % (D / 4);
-      *(float4*)&s_km[c][4 * k4] = *(const float4*)(km + ((int64_t)a.seg_slot[c] * a.bh + bh) * D + 4 * k4);
-    }
-  }
-  float x[64];
+  const int64_t row0 = (int64_t)grp * QG;
+  const uint16_t* qp = q + b * a.sb + h * a.sh + g * 8;
+  uint32_t x[2][4][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const v4i w = ok ? *(const v4i*)(qp + 8 * i) : v4i{0, 0, 0, 0};
-    unpack8(w, x + 8 * i);
-  }
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < 64; ++i) amax = fmaxf(amax, fabsf(x[i]));
-  amax = fmaxf(wave_max(amax), AMAX_FLOOR);
-  const float recip = __fdiv_rn(127.f, amax);
-  if (lane == 0) q_scale[(int64_t)bh * (a.lp / QG) + grp] = __fdiv_rn(amax, 127.f);
-  int8_t* out = q8 + ((int64_t)bh * a.lp + row) * D + half * 64;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int w[4];
+  for (int s = 0; s < 2; ++s)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t u = 0;
+      const int64_t t = row0 + 4 * (rq + 4 * s) + j;
+      const v4i v = t < a.lq ? *(const v4i*)(qp + t * a.st) : v4i{0, 0, 0, 0};
 #pragma unroll
-      for (int c = 0; c < 4; ++c) u |= ((uint32_t)quant_i8(x[16 * i + 4 * j + c], recip) & 0xFFu) << (8 * c);
-      w[j] = (int)u;
+      for (int c = 0; c < 4; ++c) x[s][j][c] = (uint32_t)v[c];
     }
-    *(v4i*)(out + 16 * i) = v4i{w[0], w[1], w[2], w[3]};
-  }
-  if (a.n_seg > 1) {
-    __syncthreads();   // s_km is filled (one wave: orders the LDS writes before the reads)
-    for (int c = 0; c < a.n_seg; ++c) {
-      const float* m = &s_km[c][half * 64];
-      float acc = 0.f;
+  float amax = 0.f;
 #pragma unroll
-      for (int i = 0; i < 64; ++i) acc = fmaf(x[i], m[i], acc);
-      acc += __shfl_xor(acc, 1);
-      if (half == 0) bias[((int64_t)c * a.bh + bh) * a.lp + row] = acc;
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(x[s][j][c] << 16)),
+                                 fabsf(__uint_as_float(x[s][j][c] & 0xFFFF0000u))));
+  amax = fmaxf(wave_max(amax), AMAX_FLOOR);
+  const float recip = __fdiv_rn(127.f, amax);
+  if (lane == 0) q_scale[bh * (a.lp / QG) + grp] = __fdiv_rn(amax, 127.f);
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = row0 + 4 * (rq + 4 * s) + j;
+      uint32_t wd[2];
+#pragma unroll
+      for (int hw = 0; hw < 2; ++hw) {
+        const uint32_t u0 = x[s][j][2 * hw], u1 = x[s][j][2 * hw + 1];
+        wd[hw] = ((uint32_t)quant_i8(__uint_as_float(u0 << 16), recip) & 0xFFu) |
+                 (((uint32_t)quant_i8(__uint_as_float(u0 & 0xFFFF0000u), recip) & 0xFFu) << 8) |
+                 (((uint32_t)quant_i8(__uint_as_float(u1 << 16), recip) & 0xFFu) << 16) |
+                 (((uint32_t)quant_i8(__uint_as_float(u1 & 0xFFFF0000u), recip) & 0xFFu) << 24);
+      }
+      *(uint2*)(q8 + (bh * a.lp + t) * D + g * 8) = make_uint2(wd[0], wd[1]);
     }
+  for (int c = 0; a.n_seg > 1 && c < a.n_seg; ++c) {
+    const float* m = km + ((int64_t)a.seg_slot[c] * a.bh + bh) * D + g * 8;
+    const float4 m0 = *(const float4*)m, m1 = *(const float4*)(m + 4);
+    const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc = fmaf(__uint_as_float(x[s][j][e] << 16), mv[2 * e], acc);
+          acc = fmaf(__uint_as_float(x[s][j][e] & 0xFFFF0000u), mv[2 * e + 1], acc);
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o);
+        if (g == 0) bias[((int64_t)c * a.bh + bh) * a.lp + row0 + 4 * (rq + 4 * s) + j] = acc;
+      }
   }
 }
 
@@ -99,8 +117,8 @@ extern "C" int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t
   }
   if (a.lp / QG > 0x7fffffff) return LBW_E_SHAPE;
   if (const int dv = check_device()) return dv;
-  hipLaunchKernelGGL(quant_q_kernel, dim3((unsigned)(a.lp / QG), (unsigned)a.bh), dim3(64), 0,
-                     (hipStream_t)stream, q, a, q8, q_scale, km, bias);
+  hipLaunchKernelGGL(quant_q_kernel, dim3((unsigned)(a.lp / QG), (unsigned)((a.bh + QQ_WAVES - 1) / QQ_WAVES)),
+                     dim3(64 * QQ_WAVES), 0, (hipStream_t)stream, q, a, q8, q_scale, km, bias);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }
