@@ -347,7 +347,9 @@ DIM, FFN = 1536, 8960       # the DiT's model and feed-forward widths
 def fp8_linear_calls(dev, steps=30):
     """The DiT's FP8 linears at the chunk shape (6032 tokens): q/k/v/o (1536 -> 1536) and the two feed-forward
     layers (1536 -> 8960, 8960 -> 1536). Per call: the activation quantisation (lbw_quant_rows_fp8) and
-    hipBLASLt's rowwise-scaled FP8 GEMM with the bias. Flops 2 M K N against 5.0 PFLOP/s dense fp8."""
+    hipBLASLt's rowwise-scaled FP8 GEMM with the bias. Flops 2 M K N against 5.0 PFLOP/s dense fp8.
+    act_quant_call_ms times the quantisation call alone from Python; at ~6-9 us of kernel time it is bound by the
+    launch path, so it is an upper bound on the kernel."""
     import torch
     from lingbot_world_v2_realtime_amd import kernels
     from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear
@@ -365,7 +367,7 @@ def fp8_linear_calls(dev, steps=30):
         q_ms = _timed(lambda: kernels.quant_rows_fp8(x.view(LQ, k)), steps, stream)
         flops = 2.0 * LQ * k * n
         tf = flops / (ms * 1e-3) / 1e12
-        out[name] = {"ms": round(ms, 4), "act_quant_ms": round(q_ms, 4), "TFLOP/s": round(tf, 1),
+        out[name] = {"ms": round(ms, 4), "act_quant_call_ms": round(q_ms, 4), "TFLOP/s": round(tf, 1),
                      "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
     return out
 
