@@ -369,6 +369,18 @@ def fp8_linear_calls(dev, steps=30):
         tf = flops / (ms * 1e-3) / 1e12
         out[name] = {"ms": round(ms, 4), "act_quant_call_ms": round(q_ms, 4), "TFLOP/s": round(tf, 1),
                      "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+    # the MXFP8 mode (per-32 E8M0 scales) at the projection shape: its GEMM pads the rows to 128
+    from lingbot_world_v2_realtime_amd.layers.linear import MXFP8Linear
+    lin = torch.nn.Linear(DIM, DIM).to(torch.bfloat16).to(dev)
+    f = MXFP8Linear(lin)
+    x = torch.randn(1, LQ, DIM, device=dev).to(torch.bfloat16)
+    for _ in range(3):
+        f(x)
+    torch.cuda.synchronize()
+    ms = _timed(lambda: f(x), steps, torch.cuda.current_stream(dev))
+    tf = 2.0 * LQ * DIM * DIM / (ms * 1e-3) / 1e12
+    out["mx_proj_1536x1536"] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1),
+                                "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
     return out
 
 

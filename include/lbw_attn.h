@@ -164,6 +164,16 @@ int lbw_quant_rows_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t cols,
                        uint8_t* x8, float* scale, void* stream);
 
 /*
+ * MXFP8 quantisation of x [rows][cols] (bf16, or fp32 when x_is_fp32; row stride s_row; cols a multiple of 32):
+ * per 32 consecutive values, scale = 2^e, e = ceil(log2(max(amax, 2^-126) / 448)) (exact, floored at -127),
+ * x8 = e4m3(x / scale) and scale_e8m0 = e + 127, rows packed (x8 [rows_pad][cols], scale_e8m0
+ * [rows_pad][cols / 32]); rows rows .. rows_pad - 1 are written as zeros with scale byte 127. The quantisation of
+ * lingbot/layers/linear.py:42-50 (MXFP8Linear), for a GEMM whose row count is padded to its tile.
+ */
+int lbw_quant_mx_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t rows_pad, int64_t cols, int64_t s_row,
+                     uint8_t* x8, uint8_t* scale_e8m0, void* stream);
+
+/*
  * Quantized attention of Q (from lbw_quant_q) over the chunks seg_slot[0..n_seg) of one layer's cache
  * (pointers already offset to that layer), chunk c holding seg_len[c] valid tokens (1..cap). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the

@@ -65,6 +65,67 @@ __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict
   }
 }
 
+// MXFP8 (the reference's MXFP8Linear, lingbot/layers/linear.py:42-50): per 32 consecutive values of a row,
+// scale = 2^e with e = ceil(log2(max(amax, 2^-126) / 448)) taken exactly from the bits of the fp32 quotient
+// (floored at -127, E8M0's smallest), values e4m3(x / scale) (exact division by a power of two, then round to
+// nearest even), and the E8M0 byte e + 127. One thread per 32-value group; rows from `rows` up to `rows_pad` are
+// written as zeros with scale byte 127 (2^0), so the GEMM can take a row count padded to its tile.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_mx_fp8_kernel(const T* __restrict__ x, int64_t rows, int64_t rows_pad,
+                                                           int64_t cols, int64_t s_row, uint8_t* __restrict__ x8,
+                                                           uint8_t* __restrict__ e8) {
+  const int64_t groups = cols / 32;
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= rows_pad * groups) return;
+  const int64_t row = id / groups, grp = id - row * groups;
+  uint8_t* out = x8 + row * cols + grp * 32;
+  if (row >= rows) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) *(v4i*)(out + 16 * i) = v4i{0, 0, 0, 0};
+    e8[id] = 127;
+    return;
+  }
+  float f[32];
+  const T* xr = x + row * s_row + grp * 32;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) Row8<T>::load(xr + 8 * i, f + 8 * i);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(f[i]));
+  amax = fmaxf(amax, 0x1p-126f);
+  const float qv = __fdiv_rn(amax, FP8_MAX);
+  // exact ceil(log2(qv)) of a positive float: the exponent of its top bit, plus one unless qv is a power of two
+  const uint32_t qb = __float_as_uint(qv);
+  int e;
+  if ((qb >> 23) == 0) {   // subnormal quotient: value = m * 2^-149
+    const uint32_t m = qb & 0x7FFFFFu;
+    const int top = 31 - __builtin_clz(m);
+    e = top - 149 + ((m & (m - 1)) ? 1 : 0);
+  } else {
+    e = (int)(qb >> 23) - 127 + ((qb & 0x7FFFFFu) ? 1 : 0);
+  }
+  e = e < -127 ? -127 : e;
+  // 1 / 2^e as a float (2^-e, e in [-127, 127]); x * 2^-e is exact for every finite x here
+  const float inv = e >= -126 ? __uint_as_float((uint32_t)(127 - e) << 23) : 0x1p127f;
+  e8[id] = (uint8_t)(e + 127);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int b0 = 16 * i + 4 * k;
+      const float y0 = fminf(fmaxf(f[b0] * inv, -FP8_MAX), FP8_MAX);
+      const float y1 = fminf(fmaxf(f[b0 + 1] * inv, -FP8_MAX), FP8_MAX);
+      const float y2 = fminf(fmaxf(f[b0 + 2] * inv, -FP8_MAX), FP8_MAX);
+      const float y3 = fminf(fmaxf(f[b0 + 3] * inv, -FP8_MAX), FP8_MAX);
+      int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+      pk = __builtin_amdgcn_cvt_pk_fp8_f32(y2, y3, pk, true);
+      w[k] = (uint32_t)pk;
+    }
+    *(v4i*)(out + 16 * i) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
+}
+
 }  // namespace lbw
 
 using namespace lbw;
@@ -82,6 +143,25 @@ extern "C" int lbw_quant_rows_fp8(const void* x, int x_is_fp32, int64_t rows, in
   else
     hipLaunchKernelGGL(quant_rows_fp8_kernel<uint16_t>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
                        (const uint16_t*)x, cols, s_row, x8, scale);
+  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
+  return LBW_OK;
+}
+
+extern "C" int lbw_quant_mx_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t rows_pad, int64_t cols,
+                                int64_t s_row, uint8_t* x8, uint8_t* scale_e8m0, void* stream) {
+  if (!x || !x8 || !scale_e8m0) return LBW_E_NULL;
+  if (rows <= 0 || rows_pad < rows || cols <= 0 || cols % 32 != 0 || s_row < cols) return LBW_E_SHAPE;
+  if (rows_pad > ((int64_t)1 << 31) || rows_pad * (cols / 32) > ((int64_t)1 << 38)) return LBW_E_SHAPE;
+  if (s_row % 8 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)x8 & 15)) return LBW_E_ALIGN;
+  if (const int dv = check_device()) return dv;
+  const int64_t n = rows_pad * (cols / 32);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (x_is_fp32)
+    hipLaunchKernelGGL(quant_mx_fp8_kernel<float>, grid, dim3(256), 0, (hipStream_t)stream, (const float*)x, rows,
+                       rows_pad, cols, s_row, x8, scale_e8m0);
+  else
+    hipLaunchKernelGGL(quant_mx_fp8_kernel<uint16_t>, grid, dim3(256), 0, (hipStream_t)stream, (const uint16_t*)x,
+                       rows, rows_pad, cols, s_row, x8, scale_e8m0);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }

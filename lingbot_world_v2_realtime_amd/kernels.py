@@ -292,6 +292,27 @@ def quant_rows_fp8(x):
     return x8, scale
 
 
+def quant_mx_fp8(x, rows_pad=None):
+    """MXFP8 of a 2-d bf16 / fp32 device tensor x [rows, cols] (cols a multiple of 32, unit column stride):
+    (x8 float8_e4m3fn [rows_pad, cols], scale float8_e8m0fnu [rows_pad, cols / 32]), one power-of-two scale per 32
+    values; rows past `rows` (up to rows_pad, default rows) are zero with scale 1."""
+    lib = _lib.load()
+    if not x.is_cuda:
+        raise ValueError("x must be a device tensor (the FP8 path has no CPU implementation)")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be bfloat16 or float32, got {x.dtype}")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError(f"x must be 2-d with contiguous rows, got {tuple(x.shape)} / {x.stride()}")
+    rows, cols = x.shape
+    rows_pad = rows if rows_pad is None else int(rows_pad)
+    x8 = torch.empty(rows_pad, cols, dtype=torch.float8_e4m3fn, device=x.device)
+    e8 = torch.empty(rows_pad, cols // 32, dtype=torch.uint8, device=x.device)
+    st = lib.lbw_quant_mx_fp8(_ptr(x), int(x.dtype == torch.float32), rows, rows_pad, cols, x.stride(0), _ptr(x8),
+                              _ptr(e8), _stream(x))
+    _lib.check(st, "lbw_quant_mx_fp8")
+    return x8, e8.view(torch.float8_e8m0fnu)
+
+
 _ATTN_WS = {}
 
 

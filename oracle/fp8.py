@@ -16,3 +16,26 @@ def quant_rows(x):
 
 def dequant_rows(bits, scale):
     return bits.view(torch.float8_e4m3fn).float() * scale
+
+
+def quant_mx(x):
+    """MXFP8 (lingbot/layers/linear.py:42-50) with the scale exponent taken exactly: x [rows, cols] bf16 / fp32,
+    cols a multiple of 32 -> (e4m3 bits uint8 [rows, cols], E8M0 bytes uint8 [rows, cols / 32]). Per 32 values:
+    q = fp32(max(amax, 2^-126) / 448), e = ceil(log2(q)) from q's frexp (f = 0.5 exactly: a power of two),
+    floored at -127; values e4m3(x / 2^e). The reference evaluates ceil(log2(q)) in fp32, which agrees except when
+    q is within an ulp above a power of two and its log2 rounds down onto the integer."""
+    m, k = x.shape
+    xb = x.float().view(m, k // 32, 32)
+    amax = xb.abs().amax(-1).clamp(min=2.0 ** -126)
+    q = amax / torch.tensor(FMAX, dtype=torch.float32)
+    f, ex = torch.frexp(q)
+    e = torch.where(f == 0.5, ex - 1, ex).clamp(min=-127)
+    scale = torch.ldexp(torch.ones_like(q), e)
+    y = (xb / scale[..., None]).clamp(-FMAX, FMAX)
+    return y.to(torch.float8_e4m3fn).view(torch.uint8).view(m, k), (e + 127).to(torch.uint8)
+
+
+def dequant_mx(bits, e8):
+    m, k = bits.shape
+    v = bits.view(torch.float8_e4m3fn).float().view(m, k // 32, 32)
+    return (v * torch.ldexp(torch.ones(m, k // 32), e8.long() - 127)[..., None]).view(m, k)

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declarations_are_bound_and_exported(lib):
     decl = declared_functions()
-    assert len(decl) == 16
+    assert len(decl) == 17
     assert set(decl) == set(_lib.SIGNATURES)
     for name, n in decl.items():
         assert len(_lib.SIGNATURES[name][1]) == n, name
@@ -195,6 +195,15 @@ def test_quant_rows_fp8_argument_checks(lib):
     assert q(x=FAKE + 8) == E_ALIGN
     if hip_device_count() == 0:
         assert q() == E_DEVICE
+    mx = lambda **kw: lib.lbw_quant_mx_fp8(kw.get("x", FAKE), 0, kw.get("rows", 10), kw.get("pad", 128),  # noqa: E731
+                                           kw.get("cols", 256), kw.get("s", 256), kw.get("x8", FAKE), FAKE, None)
+    assert mx(x=None) == E_NULL
+    assert mx(cols=48) == E_SHAPE          # whole 32-value groups
+    assert mx(pad=5) == E_SHAPE            # the padded row count holds every row
+    assert mx(s=200) == E_SHAPE
+    assert mx(x8=FAKE + 8) == E_ALIGN
+    if hip_device_count() == 0:
+        assert mx() == E_DEVICE
 
 
 def attn(lib, **kw):

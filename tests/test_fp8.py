@@ -55,3 +55,55 @@ def test_bf16_and_fp32_inputs_agree_on_bf16_values():
     b1, s1 = fp8.quant_rows(x)
     b2, s2 = fp8.quant_rows(x.float())
     assert torch.equal(b1, b2) and torch.equal(s1, s2)
+
+
+def _ref_mx_formula(x):
+    """The reference's MXFP8 quantiser as written (lingbot/layers/linear.py:42-50): the exponent through fp32
+    log2 / ceil / exp2."""
+    m, k = x.shape
+    xb = x.float().view(m, k // 32, 32)
+    amax = xb.abs().amax(-1, keepdim=True).clamp(min=2.0 ** -126)
+    scale = torch.exp2(torch.ceil(torch.log2(amax / 448)))
+    q = (xb / scale).to(torch.float8_e4m3fn).view(m, k)
+    return q.view(torch.uint8), scale.view(m, k // 32)
+
+
+def test_mx_matches_the_reference_formula_away_from_power_of_two_boundaries():
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(200, 512, generator=g) * torch.exp(torch.randn(200, 16, 1, generator=g) * 3).repeat_interleave(32, 1).view(200, 512))
+    x = x.to(torch.bfloat16)
+    bits, e8 = fp8.quant_mx(x)
+    rb, rs = _ref_mx_formula(x)
+    scale = torch.ldexp(torch.ones(e8.shape), e8.long() - 127)
+    assert torch.equal(scale, rs)          # random groups never land within an ulp of a boundary
+    assert torch.equal(bits, rb)
+
+
+def test_mx_exact_exponent_at_a_boundary():
+    """amax / 448 one ulp above 2^k: the exact ceil is k + 1 (so x / scale stays <= 448); fp32 log2 may round
+    onto k. A group whose amax / 448 is exactly 2^k gets scale 2^k and its max maps to 448."""
+    x = torch.zeros(2, 32)
+    x[0, 0] = 448.0 * 2.0 ** -3                           # q = 2^-3 exactly
+    q1 = torch.nextafter(torch.tensor(2.0 ** -3), torch.tensor(1.0))
+    x[1, 0] = (q1 * 448).item()
+    bits, e8 = fp8.quant_mx(x)
+    assert e8[0, 0].item() == 127 - 3 and bits[0, 0].view(torch.float8_e4m3fn).item() == 448.0
+    qv = (x[1, 0] / torch.tensor(448.0)).item()
+    if qv > 2.0 ** -3:                                      # the product rounded above the power of two
+        assert e8[1, 0].item() == 127 - 2
+    dq = fp8.dequant_mx(bits, e8)
+    assert torch.equal(dq[0], x[0])
+
+
+def test_mx_grid_zero_groups_and_error_bound():
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(16, 256, generator=g)
+    x[0, :32] = 0
+    bits, e8 = fp8.quant_mx(x)
+    assert e8[0, 0].item() == 0 and torch.equal(bits[0, :32], torch.zeros(32, dtype=torch.uint8))   # 2^-127 floor
+    q = bits.view(torch.float8_e4m3fn).float()
+    grid = e4m3_values()
+    assert np.isin(np.abs(q.numpy()), grid).all() and q.abs().max().item() <= 448
+    dq = fp8.dequant_mx(bits, e8)
+    big = x.abs() > x.abs().view(16, 8, 32).amax(-1).repeat_interleave(32, 1) * 2 ** -5
+    assert ((dq - x).abs()[big] <= x.abs()[big] * 2 ** -4).all()

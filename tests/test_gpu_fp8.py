@@ -84,3 +84,49 @@ def test_convert_to_fp8_selection():
     assert (n_fp8, n_all) == (2, 4)
     assert isinstance(blk[0], FP8Linear) and isinstance(blk[1][0], FP8Linear)
     assert isinstance(blk[2], torch.nn.Linear) and isinstance(blk[3], torch.nn.Linear)
+
+
+@pytest.mark.parametrize("rows,rows_pad,cols,dtype", [(1, 128, 32, torch.bfloat16), (100, 128, 1536, torch.bfloat16),
+                                                      (6032, 6144, 1536, torch.bfloat16),
+                                                      (300, 384, 8960, torch.float32)])
+def test_quant_mx_bit_exact(rows, rows_pad, cols, dtype):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * torch.exp(torch.randn(rows, 1, generator=g) * 3)).to(dtype)
+    x[0, :64] = 0
+    x8, e8 = _k().quant_mx_fp8(x.to(DEV), rows_pad)
+    torch.cuda.synchronize()
+    rb, re = fp8.quant_mx(x)
+    assert torch.equal(x8.view(torch.uint8)[:rows].cpu(), rb)
+    assert torch.equal(e8.view(torch.uint8)[:rows].cpu(), re)
+    assert not x8.view(torch.uint8)[rows:].any() and (e8.view(torch.uint8)[rows:] == 127).all()
+
+
+@pytest.mark.parametrize("m,k,n,bias", [(6032, 1536, 1536, True), (100, 1536, 8960, False)])
+def test_mxfp8_linear(m, k, n, bias):
+    from lingbot_world_v2_realtime_amd.layers.linear import MXFP8Linear
+    g = torch.Generator().manual_seed(m + 1)
+    lin = torch.nn.Linear(k, n, bias=bias).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(n, k, generator=g) * 0.02)
+        if bias:
+            lin.bias.copy_(torch.randn(n, generator=g) * 0.1)
+    f = MXFP8Linear(lin.to(DEV))
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    y = f(x.to(DEV))
+    torch.cuda.synchronize()
+    assert y.shape == (m, n) and y.dtype == torch.bfloat16
+    xb, xe = fp8.quant_mx(x)
+    wb, we = fp8.quant_mx(lin.weight.detach().cpu())
+    ref = fp8.dequant_mx(xb, xe) @ fp8.dequant_mx(wb, we).t()
+    if bias:
+        ref = ref + lin.bias.detach().cpu().float()
+    e = (y.float().cpu() - ref).abs()
+    record(f"MXFP8Linear {m}x{k}x{n}: vs same-operand fp32 max {e.max().item():.2e} (|ref| max {ref.abs().max().item():.2e})")
+    assert e.max().item() <= 1e-2 * ref.abs().max().item()
+
+
+def test_convert_to_fp8_mx_selection():
+    from lingbot_world_v2_realtime_amd.layers.linear import MXFP8Linear, convert_to_fp8
+    blk = torch.nn.Sequential(torch.nn.Linear(1536, 1536), torch.nn.Linear(1040, 1536)).to(torch.bfloat16).to(DEV)
+    assert convert_to_fp8(blk, mx=True) == (1, 2)   # 1040 is a multiple of 16, not of 32
+    assert isinstance(blk[0], MXFP8Linear) and isinstance(blk[1], torch.nn.Linear)
