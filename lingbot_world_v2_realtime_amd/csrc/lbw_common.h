@@ -60,10 +60,57 @@ __device__ __forceinline__ int quant_i8(float x, float recip) {
   return (int)r;
 }
 
+// Cross-lane reads by DPP, within rows of 16 lanes: a VALU operand modifier, with no LDS round trip (a shuffle
+// through ds_bpermute costs an LDS instruction and its latency per step). Every source lane used here is inside
+// the row, so the row / bank masks keep all lanes.
+constexpr int DPP_XOR1 = 0xB1;          // quad_perm [1, 0, 3, 2]: lane ^ 1
+constexpr int DPP_XOR2 = 0x4E;          // quad_perm [2, 3, 0, 1]: lane ^ 2
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane 7 - i within each 8 lanes
+constexpr int DPP_MIRROR = 0x140;       // lane 15 - i within each 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) { return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(x))); }
+template <int CTRL>
+__device__ __forceinline__ double dpp(double x) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint64_t lo = dpp_u32<CTRL>((uint32_t)u), hi = dpp_u32<CTRL>((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(lo | (hi << 32)));
+}
+
+// Sum over each row of 16 lanes, every lane receiving the value of the xor butterfly s += s[lane ^ o] for
+// o = 1, 2, 4, 8 in that order, bit for bit: after the first two steps the four lanes of a quad hold the same
+// bits (each addition is commutative), so the half-row mirror reads what lane ^ 4 holds; after the third, the
+// eight lanes of a half-row do, so the row mirror reads what lane ^ 8 holds.
+template <typename T>
+__device__ __forceinline__ T row16_sum(T s) {
+  s = s + dpp<DPP_XOR1>(s);
+  s = s + dpp<DPP_XOR2>(s);
+  s = s + dpp<DPP_HALF_MIRROR>(s);
+  s = s + dpp<DPP_MIRROR>(s);
+  return s;
+}
+
+// max over lanes l and l ^ 16 (v_permlane16_swap), and over l and l ^ 32 (v_permlane32_swap)
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// max over the wave's 64 lanes (exact in any order), in every lane
 __device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
+  x = fmaxf(x, dpp<DPP_XOR1>(x));
+  x = fmaxf(x, dpp<DPP_XOR2>(x));
+  x = fmaxf(x, dpp<DPP_HALF_MIRROR>(x));
+  x = fmaxf(x, dpp<DPP_MIRROR>(x));
+  return max_xor32(max_xor16(x));
 }
 
 // LBW_OK when the current device is a gfx950, else LBW_E_DEVICE (defined in lbw_abi.hip).

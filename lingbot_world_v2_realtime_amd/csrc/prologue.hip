@@ -59,6 +59,17 @@ __device__ __forceinline__ void stage_rope(double2* s_cs, const double2* __restr
   }
 }
 
+// The chunk means of the workgroup's heads (batch b) into LDS, [chunk][head][channel]: loaded with the rows and
+// the rope table, so the logit bias at the end waits for no global load.
+__device__ __forceinline__ void stage_means(float4* s_km, const float* __restrict__ km, const ProArgs& a, int64_t b) {
+  const int per_chunk = (int)a.heads * (D / 4);
+  for (int i = threadIdx.x; i < a.n_seg * per_chunk; i += blockDim.x) {
+    const int c = i / per_chunk, r = i - c * per_chunk, hh = r / (D / 4), u = r - hh * (D / 4);
+    s_km[(c * PRO_MAX_HEADS + hh) * (D / 4) + u] =
+        *(const float4*)(km + ((int64_t)a.seg_slot[c] * a.bh + b * a.heads + hh) * D + 4 * u);
+  }
+}
+
 // Two bf16 (low half first) <-> two fp32. The rounding is v_cvt_pk_bf16_f32 (round to nearest even, the same
 // bits as the integer rounding of the other kernels for every finite value), one instruction for two values.
 typedef __bf16 pbf2 __attribute__((ext_vector_type(2)));
@@ -107,11 +118,9 @@ __device__ __forceinline__ void norm_rope_rows(uint32_t (&x)[2][4][4], const uin
       ss[s][j] = acc;
     }
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1)
+  for (int s = 0; s < 2; ++s)
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) ss[s][j] = ss[s][j] + __shfl_xor(ss[s][j], o);
+    for (int j = 0; j < 4; ++j) ss[s][j] = row16_sum(ss[s][j]);
   if (g == 0)
 #pragma unroll
     for (int s = 0; s < 2; ++s)
@@ -161,6 +170,7 @@ __global__ __launch_bounds__(MAXT) void norm_rope_q_kernel(const uint16_t* __res
   __shared__ double2 s_cs[PR * RP];
   __shared__ double s_ss[PR * PRO_MAX_HEADS];
   __shared__ float s_r[PR];
+  __shared__ float4 s_km[LBW_MAX_SEGMENTS * PRO_MAX_HEADS * (D / 4)];
   const int grp = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, rq = lane >> 4, g = lane & 15;
   const int64_t row0 = (int64_t)grp * PR;
@@ -168,6 +178,7 @@ __global__ __launch_bounds__(MAXT) void norm_rope_q_kernel(const uint16_t* __res
   uint32_t x[2][4][4];
   load_rows(x, q + b * a.x_sb, a, row0);
   stage_rope(s_cs, tab, a, row0);
+  if (a.n_seg > 1) stage_means(s_km, km, a, b);   // norm_rope_rows' barriers order the staging before the reads
   norm_rope_rows(x, w, a, s_ss, s_r, s_cs);
   float amax = 0.f;
 #pragma unroll
@@ -198,8 +209,8 @@ __global__ __launch_bounds__(MAXT) void norm_rope_q_kernel(const uint16_t* __res
             v4i{(int)x[s][j][0], (int)x[s][j][1], (int)x[s][j][2], (int)x[s][j][3]};
     }
   for (int c = 0; a.n_seg > 1 && c < a.n_seg; ++c) {
-    const float* m = km + ((int64_t)a.seg_slot[c] * a.bh + bh) * D + g * 8;
-    const float4 m0 = *(const float4*)m, m1 = *(const float4*)(m + 4);
+    const float4* m = s_km + (c * PRO_MAX_HEADS + h) * (D / 4) + 2 * g;
+    const float4 m0 = m[0], m1 = m[1];
     const float mv[8] = {m0.x, m0.y, m0.z, m0.w, m1.x, m1.y, m1.z, m1.w};
 #pragma unroll
     for (int s = 0; s < 2; ++s)
@@ -211,8 +222,7 @@ __global__ __launch_bounds__(MAXT) void norm_rope_q_kernel(const uint16_t* __res
           acc = fmaf(bf_lo(x[s][j][q]), mv[2 * q], acc);
           acc = fmaf(bf_hi(x[s][j][q]), mv[2 * q + 1], acc);
         }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o);
+        acc = row16_sum(acc);
         if (g == 0) bias[((int64_t)c * a.bh + bh) * a.lp + row0 + 4 * (rq + 4 * s) + j] = acc;
       }
   }
@@ -236,7 +246,39 @@ __global__ __launch_bounds__(MAXT) void norm_rope_k_kernel(const uint16_t* __res
   const int64_t row0 = (int64_t)half * PR;
   uint32_t x[2][4][4];
   load_rows(x, k + b * a.x_sb, a, row0);
+  // the V rows go out with the K rows; V is neither normed nor roped, so its column max |V| is taken (and
+  // written) as soon as they land, before the rope needs the registers
+  v4i vw[2][4];
+  const uint16_t* vp = v + b * a.v_sb + h * a.v_sh + g * 8;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = row0 + 4 * (rq + 4 * s) + j;
+      vw[s][j] = t < a.len ? *(const v4i*)(vp + (uint32_t)t * (uint32_t)a.v_st) : v4i{0, 0, 0, 0};
+    }
   stage_rope(s_cs, tab, a, row0);
+  // partials [batch * heads][blocks][2 halves][128]: half index = blockIdx.x
+  const int64_t o = (((int64_t)b * a.heads + h) * a.nb * 2 + half) * D + g * 8;
+  {   // column max |V| of the half: lane (rq, g) over its 8 rows, then over rq (lanes g + 16 rq)
+    float vmax[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vmax[e] = 0.f;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          vmax[2 * q] = fmaxf(vmax[2 * q], fabsf(bf_lo((uint32_t)vw[s][j][q])));
+          vmax[2 * q + 1] = fmaxf(vmax[2 * q + 1], fabsf(bf_hi((uint32_t)vw[s][j][q])));
+        }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) vmax[e] = max_xor32(max_xor16(vmax[e]));
+    if (rq == 0)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part_amax[o + e] = vmax[e];
+  }
   norm_rope_rows(x, w, a, s_ss, s_r, s_cs);
   uint16_t* ko = k_out + b * a.o_sb + h * a.o_sh + g * 8;
 #pragma unroll
@@ -263,28 +305,6 @@ __global__ __launch_bounds__(MAXT) void norm_rope_k_kernel(const uint16_t* __res
             v4i{(int)x[s][j][0], (int)x[s][j][1], (int)x[s][j][2], (int)x[s][j][3]};
     }
   }
-  // column max |V| of the half: lane (rq, g) over its 8 rows, then over rq
-  float vmax[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) vmax[e] = 0.f;
-  const uint16_t* vp = v + b * a.v_sb + h * a.v_sh + g * 8;
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t t = row0 + 4 * (rq + 4 * s) + j;
-      const v4i vw = t < a.len ? *(const v4i*)(vp + (uint32_t)t * (uint32_t)a.v_st) : v4i{0, 0, 0, 0};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        vmax[2 * q] = fmaxf(vmax[2 * q], fabsf(bf_lo((uint32_t)vw[q])));
-        vmax[2 * q + 1] = fmaxf(vmax[2 * q + 1], fabsf(bf_hi((uint32_t)vw[q])));
-      }
-    }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    vmax[e] = fmaxf(vmax[e], __shfl_xor(vmax[e], 16));
-    vmax[e] = fmaxf(vmax[e], __shfl_xor(vmax[e], 32));
-  }
   __syncthreads();
   // the half's column sum over its 4-row sums in row order; lane (rq, g) takes channels 8 g + 2 rq, + 1
   const float* col = (const float*)&s_S[h][0][0] + 8 * g + 2 * rq;
@@ -294,13 +314,8 @@ __global__ __launch_bounds__(MAXT) void norm_rope_k_kernel(const uint16_t* __res
     acc0 = acc0 + col[r * D];
     acc1 = acc1 + col[r * D + 1];
   }
-  // partials [batch * heads][blocks][2 halves][128]: half index = blockIdx.x
-  const int64_t o = (((int64_t)b * a.heads + h) * a.nb * 2 + half) * D + g * 8;
   part_sum[o + 2 * rq] = acc0;
   part_sum[o + 2 * rq + 1] = acc1;
-  if (rq == 0)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) part_amax[o + e] = vmax[e];
 }
 
 // Shared argument checks of the two entry points; fills the rope / norm part of `a`.

@@ -79,8 +79,7 @@ __global__ __launch_bounds__(64 * QQ_WAVES) void quant_q_kernel(const uint16_t* 
           acc = fmaf(__uint_as_float(x[s][j][e] << 16), mv[2 * e], acc);
           acc = fmaf(__uint_as_float(x[s][j][e] & 0xFFFF0000u), mv[2 * e + 1], acc);
         }
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o);
+        acc = row16_sum(acc);
         if (g == 0) bias[((int64_t)c * a.bh + bh) * a.lp + row0 + 4 * (rq + 4 * s) + j] = acc;
       }
   }
