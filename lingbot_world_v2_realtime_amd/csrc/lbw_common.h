@@ -28,6 +28,10 @@ constexpr float RESCALE_SLACK = 2.f;
 constexpr int S_MAGIC = 0x4B400000;          // int bits of 12582912.0f = 1.5 * 2^23
 constexpr float S_MAGIC_F = 12582912.f;      // float(S_MAGIC + s) == 12582912 + s for |s| < 2^22
 
+// Loads of data that is read once: the non-temporal hint streams it through the caches without keeping it
+// (measured on MI355X: 7.0-7.3 TB/s for a 1.1 GB read against 6.3-6.4 TB/s with plain loads).
+__device__ __forceinline__ v4i load_once(const void* p) { return __builtin_nontemporal_load((const v4i*)p); }
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 // fp32 -> nearest bf16 (ties to even) as fp32; finite inputs.
