@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
       lo |= ((uint32_t)quant_i8(x[j][c], recip) & 0xFFu) << (8 * c);
       hi |= ((uint32_t)quant_i8(x[j][c + 4], recip) & 0xFFu) << (8 * c);
     }
-    *(uint2*)(kout + (kq * 4 + j) * D) = make_uint2(lo, hi);
+    store_once(kout + (kq * 4 + j) * D, v2i{(int)lo, (int)hi});
   }
   // V tiles out: thread t writes 32 contiguous bytes (channel t >> 1, positions 32 * (t & 1) ..) of each plane
   for (int pl = 0; pl < (v8lo ? 2 : 1); ++pl) {
@@ -229,8 +229,8 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
 #pragma unroll
     for (int i = 0; i < 8; ++i) w[i] = s_v[pl][ch * 16 + ((d0 + i) ^ (ch >> 3))];
     uint8_t* vout = (pl ? v8lo : v8) + (slot_bh * a.nbc + blk) * (D * KB) + ch * KB + d0 * 4;
-    *(v4i*)vout = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-    *(v4i*)(vout + 16) = v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]};
+    store_once(vout, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+    store_once(vout + 16, v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]});
   }
 }
 
