@@ -494,7 +494,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     // P^T B operand: byte 16 mt' + 4 i + j of this lane = p[16 mt' + 4 i + j] (keys 32 mt' + 8 i + 4 g + j).
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      int wd = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * r], p[4 * r + 1], 0, false);
+      // both halves of the word are written, so the previous word serves as the "old" operand (no zeroing move)
+      int wd = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * r], p[4 * r + 1], pb[r], false);
       wd = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * r + 2], p[4 * r + 3], wd, true);
       pb[r] = wd;
     }
