@@ -4,21 +4,29 @@
 //   cross_prepare_kernel: the context's K and V, [B, Lk, H, 128] bf16, into the layout the attention reads:
 //                         K [BH][Lkp][128] and V transposed, [BH][128][Lkp], keys zero-padded to Lkp = ceil64(Lk).
 //                         Done once per generation (the reference caches the cross-attention K / V the same way).
-//   cross_attn_kernel:    one workgroup per (128-query tile, batch * head), 4 waves x 32 queries, two workgroups a
-//                         CU. Per 64-key tile (two LDS stages, filled by direct global -> LDS loads one tile
+//   cross_attn_kernel:    one workgroup per (128-query tile, batch * head), 4 waves x 32 queries, three workgroups
+//                         a CU (168 registers, 48 KB of LDS each), so the DiT's 576 tiles run in one round on 768
+//                         slots. Per 32-key tile (three LDS stages, filled by direct global -> LDS loads two tiles
 //                         ahead): S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (lane = query, 16 keys per lane), an
 //                         online softmax in the exp2 domain (one FMA and one exp2 per score, the key mask only on
 //                         a ragged last tile), P^T in bf16 straight from the S^T registers into the B operand of
 //                         O^T += V^T P^T (the keys of the two products are permuted alike, so P needs no exchange
 //                         between lanes), then O / l.
+#include <type_traits>
+
 #include "lbw_common.h"
 
 namespace lbw {
 
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 
-constexpr int XQ = 128;            // queries per workgroup
-constexpr int XK = 64;             // keys per tile
+constexpr int XQ = 128;                     // queries per workgroup
+constexpr int XK = 32;                      // keys per attention tile
+constexpr int XKT = XK / 32;                // 32-key S^T products per tile
+constexpr int XNC = XK / 8;                 // 16-byte chunks per V^T row of a tile
+constexpr int XSTAGES = XK == 32 ? 3 : 2;   // LDS stages: tile t + XSTAGES - 1 loads while tile t is read
+constexpr int XOCC = XK == 32 ? 3 : 2;      // workgroups per CU (registers and LDS sized for it)
+constexpr int XPK = 64;                     // the prepared context pads its keys to a multiple of this
 constexpr int XWAVES = 4;
 constexpr int XT = XWAVES * 64;    // threads
 constexpr int XMAX_BATCH = 64;
@@ -31,14 +39,21 @@ struct XArgs {
   int klen[XMAX_BATCH];   // valid keys per batch entry (1 .. lk)
 };
 
-// Workgroup (64-key tile, batch * head): K rows copied, V transposed through LDS; keys past lk are zero.
+// Key held at position p of a 32-key span of a prepared V^T row: inside each 16-key group the middle two quarters
+// are swapped (positions 4-7 hold keys 8-11, positions 8-11 keys 4-7).
+__device__ __forceinline__ int vt_key(int p) {
+  const int qd = (p >> 2) & 3;
+  return (p & ~15) + ((qd == 1 ? 2 : qd == 2 ? 1 : qd) << 2) + (p & 3);
+}
+
+// Workgroup (64-key padding tile, batch * head): K rows copied, V transposed through LDS; keys past lk are zero.
 __global__ __launch_bounds__(256) void cross_prepare_kernel(const uint16_t* __restrict__ k,
                                                             const uint16_t* __restrict__ v, int64_t lk,
                                                             int64_t lkp, int64_t heads, int64_t k_sb,
                                                             int64_t k_st, int64_t k_sh, int64_t v_sb,
                                                             int64_t v_st, int64_t v_sh, uint16_t* __restrict__ kp,
                                                             uint16_t* __restrict__ vt) {
-  __shared__ uint16_t s_v[XK][D + 2];
+  __shared__ uint16_t s_v[XPK][D + 2];
   const int tile = blockIdx.x, bh = blockIdx.y, t = threadIdx.x;
   const int64_t b = bh / heads, h = bh % heads;
   // thread t: key 4 (t >> 4) .. + 3, channels 8 (t & 15) .. + 7
@@ -46,7 +61,7 @@ __global__ __launch_bounds__(256) void cross_prepare_kernel(const uint16_t* __re
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int kk = 4 * (t >> 4) + j;
-    const int64_t key = (int64_t)tile * XK + kk;
+    const int64_t key = (int64_t)tile * XPK + kk;
     v4i kw = {0, 0, 0, 0}, vw = {0, 0, 0, 0};
     if (key < lk) {
       kw = *(const v4i*)(k + b * k_sb + key * k_st + h * k_sh + c8);
@@ -60,12 +75,16 @@ __global__ __launch_bounds__(256) void cross_prepare_kernel(const uint16_t* __re
     }
   }
   __syncthreads();
-  // thread t: channel t >> 1, keys 32 (t & 1) .. + 31 -> 64 contiguous bytes of V^T
+  // thread t: channel t >> 1, keys 32 (t & 1) .. + 31 -> 64 contiguous bytes of V^T, each 16-key group stored
+  // in the order 0-3, 8-11, 4-7, 12-15 (vt_key): the 8 keys a PV fragment lane takes are one 16-byte chunk
   const int ch = t >> 1, k0 = (t & 1) * 32;
   uint32_t w[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) w[i] = (uint32_t)s_v[k0 + 2 * i][ch] | ((uint32_t)s_v[k0 + 2 * i + 1][ch] << 16);
-  uint16_t* dst = vt + ((int64_t)bh * D + ch) * lkp + (int64_t)tile * XK + k0;
+  for (int i = 0; i < 16; ++i) {
+    const int kk = k0 + vt_key(2 * i);   // stored positions 2 i, 2 i + 1 hold consecutive keys
+    w[i] = (uint32_t)s_v[kk][ch] | ((uint32_t)s_v[kk + 1][ch] << 16);
+  }
+  uint16_t* dst = vt + ((int64_t)bh * D + ch) * lkp + (int64_t)tile * XPK + k0;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
     *(v4i*)(dst + 8 * i) = v4i{(int)w[4 * i], (int)w[4 * i + 1], (int)w[4 * i + 2], (int)w[4 * i + 3]};
@@ -80,28 +99,45 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Global -> LDS copy of 16 bytes per lane (lane i lands at M0 + 16 i), as inline asm: the compiler's builtin is
-// modelled as a FLAT access that may touch LDS, which would make every LDS wait drain all reads in flight.
-__device__ __forceinline__ void xdma16(const void* src, uint8_t* lds) {
+// Global -> LDS copy of 16 bytes per lane (lane i lands at M0 + 16 i) from a wave-uniform base plus a 32-bit
+// per-lane byte offset (the global instruction's scalar-base form: no 64-bit address per lane), as inline asm:
+// the compiler's builtin is modelled as a FLAT access that may touch LDS, which would make every LDS wait drain
+// all reads in flight.
+__device__ __forceinline__ void xdma16(const void* base, uint32_t off, uint8_t* lds) {
   uint32_t keep;
   const uint32_t dst = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)lds;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
                "s_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(src), "s"(dst) : "memory");
+               : "=&s"(keep) : "v"(off), "s"(base), "s"(dst) : "memory");
 }
 
 // LDS tiles, XOR-swizzled by row so the fragment reads spread over the banks:
-//   K   [64 keys][256 B]: 16-byte chunk c of row r sits at position c ^ (r & 15)
-//   V^T [128 channels][128 B]: chunk c of row r sits at position c ^ ((r >> 1) & 7)
-constexpr int XK_TILE = XK * D * 2;          // 16 KB
-constexpr int XV_TILE = D * XK * 2;          // 16 KB
+//   K   [XK keys][256 B]: 16-byte chunk c of row r sits at position c ^ (r & 15)
+//   V^T [128 channels][2 XK B]: chunk c of row r sits at position c ^ vswz(r), so the 16 rows a fragment read
+//       serves at a time cover 16 distinct (row offset, position) bank groups
+constexpr int XK_TILE = XK * D * 2;
+constexpr int XV_TILE = D * XK * 2;
 constexpr int XSTAGE = XK_TILE + XV_TILE;
+static_assert(XSTAGES * XSTAGE * XOCC <= 163840, "LDS");
+__device__ __forceinline__ int vswz(int r) { return (r >> (XNC == 4 ? 2 : 1)) & (XNC - 1); }
 
-__global__ __launch_bounds__(XT, 2) void cross_attn_kernel(const uint16_t* __restrict__ q,
-                                                           const uint16_t* __restrict__ kp,
-                                                           const uint16_t* __restrict__ vt, XArgs a,
-                                                           uint16_t* __restrict__ out) {
-  __shared__ __align__(16) uint8_t xlds[2 * XSTAGE];
+// s_waitcnt on vmcnt only (lgkmcnt and expcnt at their maxima): vmcnt(n) for n = 0 .. 15
+__device__ __forceinline__ void xwait_vm(int n) {
+  switch (n) {
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+  }
+}
+
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+__global__ __launch_bounds__(XT, XOCC) void cross_attn_kernel(const uint16_t* __restrict__ q,
+                                                              const uint16_t* __restrict__ kp,
+                                                              const uint16_t* __restrict__ vt, XArgs a,
+                                                              uint16_t* __restrict__ out) {
+  __shared__ __align__(16) uint8_t xlds[XSTAGES * XSTAGE];
   const int qt = blockIdx.x, bh = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, hf = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -121,19 +157,39 @@ __global__ __launch_bounds__(XT, 2) void cross_attn_kernel(const uint16_t* __res
     for (int s = 0; s < 8; ++s) qf[s] = as_bf8(qrow < a.lq ? *(const v4i*)(qp + 16 * s) : v4i{0, 0, 0, 0});
   }
 
-  // DMA: wave w moves K rows 16 w .. 16 w + 15 (4 x 1 KB) and V^T rows 32 w .. 32 w + 31 (4 x 1 KB) of a tile
+  // DMA: wave w moves K rows (XK / 4) w .. + XK / 4 and V^T rows 32 w .. 32 w + 31 of a tile, 1 KB per
+  // instruction, XK / 16 of each a wave per tile; byte offsets from the tile's scalar base below 2^31
+  constexpr int NDMA = XK / 16;
+  constexpr int VROWS = 1024 / (2 * XK);   // V^T rows per 1 KB
+  uint32_t koff[NDMA], voff[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int r = (XK / 4) * w + 4 * i + (lane >> 4), p = lane & 15;
+    koff[i] = (uint32_t)(r * (D * 2) + ((p ^ (r & 15)) << 4));
+    const int rv = 32 * w + VROWS * i + lane / XNC, pv = lane % XNC;
+    voff[i] = (uint32_t)(rv * vrow_bytes + ((pv ^ vswz(rv)) << 4));
+  }
   auto issue = [&](int tl, int stg) {
     uint8_t* sk = xlds + stg * XSTAGE;
     uint8_t* sv = sk + XK_TILE;
+    const uint8_t* kt_base = kbase + (int64_t)tl * XK_TILE;
+    const uint8_t* vt_base = vbase + (int64_t)tl * (XK * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 16 * w + 4 * i + (lane >> 4), p = lane & 15;
-      xdma16(kbase + ((int64_t)tl * XK + r) * (D * 2) + ((p ^ (r & 15)) << 4), sk + (16 * w + 4 * i) * 256);
-      const int rv = 32 * w + 8 * i + (lane >> 3), pv = lane & 7;
-      xdma16(vbase + rv * vrow_bytes + (int64_t)tl * (XK * 2) + ((pv ^ ((rv >> 1) & 7)) << 4),
-             sv + (32 * w + 8 * i) * 128);
+    for (int i = 0; i < NDMA; ++i) {
+      xdma16(kt_base, koff[i], sk + ((XK / 4) * w + 4 * i) * 256);
+      xdma16(vt_base, voff[i], sv + (32 * w + VROWS * i) * (2 * XK));
     }
   };
+
+  // fragment read offsets inside a stage: K chunk 2 st + hf of row lq; V^T chunk 4 kt + 2 u + hf of row lq
+  // (the rows of further products follow at fixed distances)
+  int kro[8], vro[XKT][2];
+#pragma unroll
+  for (int st = 0; st < 8; ++st) kro[st] = lq * 256 + (((2 * st + hf) ^ (lq & 15)) << 4);
+#pragma unroll
+  for (int kt = 0; kt < XKT; ++kt)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) vro[kt][u] = XK_TILE + lq * (2 * XK) + (((4 * kt + 2 * u + hf) ^ vswz(lq)) << 4);
 
   v16f o[4];
 #pragma unroll
@@ -142,48 +198,53 @@ __global__ __launch_bounds__(XT, 2) void cross_attn_kernel(const uint16_t* __res
     for (int i = 0; i < 16; ++i) o[mt][i] = 0.f;
   float m_ref = -INFINITY, l_run = 0.f;
 
-  issue(0, 0);
-  for (int tl = 0; tl < ntile; ++tl) {
-    const int stg = tl & 1;
-    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's pieces of tile tl have landed
-    __syncthreads();                      // ... and every wave's; every wave is done with the other stage
-    if (tl + 1 < ntile) issue(tl + 1, stg ^ 1);
-    const uint8_t* sk = xlds + stg * XSTAGE;
-    const uint8_t* sv = sk + XK_TILE;
+#pragma unroll
+  for (int i = 0; i < XSTAGES - 1; ++i)
+    if (i < ntile) issue(i, i);
+  // the Q fragments are complete before the loop (the compiler waits here, for the DMAs issued above as well:
+  // its own wait at the first product inside the loop would otherwise also wait for later tiles' DMAs)
+  asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]), "+v"(qf[6]),
+               "+v"(qf[7]));
+
+  // one tile in stage S (a constant, so every LDS address is a register plus an immediate)
+  auto tile = [&](int tl, auto stage) {
+    constexpr int S = decltype(stage)::value;
+    // this wave's pieces of tile tl have landed (those of the tiles after it may be in flight)
+    const int ahead = min(ntile - 1 - tl, XSTAGES - 2);
+    xwait_vm(ahead > 0 ? 2 * NDMA * ahead : 0);
+    __syncthreads();   // ... and every wave's; every wave is done with tile tl - 1's stage
+    if (tl + XSTAGES - 1 < ntile) issue(tl + XSTAGES - 1, (S + XSTAGES - 1) % XSTAGES);
+    const uint8_t* sb = xlds + S * XSTAGE;
     // S^T of keys 32 kt .. + 31: lane (lq, hf) value i is key 32 kt + 8 (i >> 2) + 4 hf + (i & 3)
-    v16f s[2];
+    v16f s[XKT];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      v16f acc;
+    for (int kt = 0; kt < XKT; ++kt) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-      const int r = 32 * kt + lq;
-      const uint8_t* kr = sk + r * 256;
+      for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
 #pragma unroll
       for (int st = 0; st < 8; ++st)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(*(const v4i*)(kr + (((2 * st + hf) ^ (r & 15)) << 4))),
-                                                      qf[st], acc, 0, 0, 0);
-      s[kt] = acc;
+        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(*(const v4i*)(sb + kt * 32 * 256 + kro[st])),
+                                                        qf[st], s[kt], 0, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);   // the phases stay apart: reads hoisted across them cost registers
     if ((tl + 1) * XK > klen) {   // the ragged last tile: keys past klen drop out
       const int kb = tl * XK + 4 * hf;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < XKT; ++kt)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           if (kb + 32 * kt + 8 * (i >> 2) + (i & 3) >= klen) s[kt][i] = -INFINITY;
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < XKT; ++kt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.sl2;   // exp2 domain; finite: every tile holds a valid key
+    mx = max_xor32(mx) * a.sl2;   // exp2 domain; finite: every tile holds a valid key
     // the exact running max: the row's largest P is exactly 1, which keeps its bf16 rounding error at zero (a
     // reference max that moves only by steps measured 19 % more mean error on a peaked softmax)
     const float m_new = fmaxf(m_ref, mx);
     const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);   // m_ref = -inf at the first tile: 0
-    l_run *= alpha;
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -193,38 +254,44 @@ __global__ __launch_bounds__(XT, 2) void cross_attn_kernel(const uint16_t* __res
     // P = exp2(s sl2 - m) <= 1, on v_exp_f32 itself (exp2f adds a compare, a select and a v_ldexp per value to
     // keep results below 2^-126 exact; weights that small do not matter next to the row's largest, exactly 1)
     const float nm = -m_ref;
-    v4i pf[2][2];
+    v4i pf[XKT][2];
+    float ps[XKT][2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < XKT; ++kt)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         float p[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          p[j] = __builtin_amdgcn_exp2f(fmaf(s[kt][8 * u + j], a.sl2, nm));
-          l_run += p[j];
-        }
+        for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(s[kt][8 * u + j], a.sl2, nm));
+        ps[kt][u] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
         pf[kt][u] = v4i{(int)pack_bf16(p[0], p[1]), (int)pack_bf16(p[2], p[3]), (int)pack_bf16(p[4], p[5]),
                         (int)pack_bf16(p[6], p[7])};
       }
-    // O^T += V^T P^T: A = V^T row 32 mt + lq, the lane's 8 keys of (kt, u) as two 8-byte pieces
+    float lt = ps[0][0] + ps[0][1];
+    if (XKT > 1) lt += ps[XKT - 1][0] + ps[XKT - 1][1];
+    l_run = fmaf(l_run, alpha, lt);
+    __builtin_amdgcn_sched_barrier(0);
+    // O^T += V^T P^T: A = V^T row 32 mt + lq, the lane's 8 keys of (kt, u): one 16-byte chunk (the prepared
+    // V^T stores each 16-key group in the fragment order)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int r = 32 * mt + lq, sw = (r >> 1) & 7;
-      const uint8_t* vr = sv + r * 128 + 8 * hf;
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < XKT; ++kt)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-          const int c = 4 * kt + 2 * u;   // 16-byte chunks c and c + 1 hold keys 32 kt + 16 u + 0..7 and + 8..15
-          const uint2 lo = *(const uint2*)(vr + ((c ^ sw) << 4));
-          const uint2 hi = *(const uint2*)(vr + (((c + 1) ^ sw) << 4));
-          const v4i vf = {(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+          const v4i vf = *(const v4i*)(sb + mt * 32 * (2 * XK) + vro[kt][u]);
           o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), as_bf8(pf[kt][u]), o[mt], 0, 0, 0);
         }
-    }
+  };
+  for (int tl = 0; tl < ntile; tl += XSTAGES) {
+    tile(tl, ic<0>{});
+    if (tl + 1 < ntile) tile(tl + 1, ic<1>{});
+    if (XSTAGES > 2 && tl + 2 < ntile) tile(tl + 2, ic<(XSTAGES > 2 ? 2 : 0)>{});
   }
-  l_run += __shfl_xor(l_run, 32);
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    l_run = __uint_as_float(r[0]) + __uint_as_float(r[1]);   // both halves of the query's keys
+  }
   if (qrow >= a.lq) return;
   const float inv_l = 1.f / l_run;
   uint16_t* op = out + b * a.o_sb + qrow * a.o_st + h * a.o_sh;
@@ -253,8 +320,8 @@ extern "C" int lbw_cross_prepare(const uint16_t* k, const uint16_t* v, int64_t b
     if (s % 8 != 0) return LBW_E_ALIGN;
   if (((uintptr_t)k | (uintptr_t)v | (uintptr_t)k_prep | (uintptr_t)vt_prep) & 15) return LBW_E_ALIGN;
   if (const int dv = check_device()) return dv;
-  const int64_t lkp = (lk + XK - 1) / XK * XK;
-  hipLaunchKernelGGL(cross_prepare_kernel, dim3((unsigned)(lkp / XK), (unsigned)(batch * heads)), dim3(256), 0,
+  const int64_t lkp = (lk + XPK - 1) / XPK * XPK;
+  hipLaunchKernelGGL(cross_prepare_kernel, dim3((unsigned)(lkp / XPK), (unsigned)(batch * heads)), dim3(256), 0,
                      (hipStream_t)stream, k, v, lk, lkp, heads, k_s_batch, k_s_tok, k_s_head, v_s_batch, v_s_tok,
                      v_s_head, k_prep, vt_prep);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
@@ -276,7 +343,7 @@ extern "C" int lbw_cross_attn_fwd(const uint16_t* q, int64_t batch, int64_t lq, 
     if (s % 8 != 0) return LBW_E_ALIGN;
   if (((uintptr_t)q | (uintptr_t)k_prep | (uintptr_t)vt_prep | (uintptr_t)out) & 15) return LBW_E_ALIGN;
   XArgs a;
-  a.lq = lq; a.lk = lk; a.lkp = (lk + XK - 1) / XK * XK; a.heads = heads; a.bh = batch * heads;
+  a.lq = lq; a.lk = lk; a.lkp = (lk + XPK - 1) / XPK * XPK; a.heads = heads; a.bh = batch * heads;
   a.q_sb = q_s_batch; a.q_st = q_s_tok; a.q_sh = q_s_head;
   a.o_sb = o_s_batch; a.o_st = o_s_tok; a.o_sh = o_s_head;
   a.sl2 = sm_scale * 1.4426950408889634f;
