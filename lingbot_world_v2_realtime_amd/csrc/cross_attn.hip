@@ -142,19 +142,23 @@ __global__ __launch_bounds__(XT, XOCC) void cross_attn_kernel(const uint16_t* __
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, hf = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int64_t b = bh / a.heads, h = bh % a.heads;
-  const int64_t qrow = (int64_t)qt * XQ + 32 * w + lq;
   const int klen = a.klen[b];
   const int ntile = (klen + XK - 1) / XK;
   const uint8_t* kbase = (const uint8_t*)(kp + (int64_t)bh * a.lkp * D);
   const uint8_t* vbase = (const uint8_t*)(vt + (int64_t)bh * D * a.lkp);
   const int64_t vrow_bytes = a.lkp * 2;
 
-  // Q^T B operand: lane (lq, hf) holds query qrow, channels 16 s + 8 hf .. + 8 (rows past lq are zero)
-  bf8 qf[8];
+  // Q rows, whole: lane -> row 4 j + lane / 16 of the wave's 32, 16-byte chunk lane & 15 (rows past lq are zero);
+  // through LDS into the Q^T B operand below
+  const int c16 = lane & 15;
+  v4i qraw[8];
   {
-    const uint16_t* qp = q + b * a.q_sb + qrow * a.q_st + h * a.q_sh + 8 * hf;
+    const uint16_t* qb = q + b * a.q_sb + h * a.q_sh + c16 * 8;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = as_bf8(qrow < a.lq ? *(const v4i*)(qp + 16 * s) : v4i{0, 0, 0, 0});
+    for (int j = 0; j < 8; ++j) {
+      const int64_t row = (int64_t)qt * XQ + 32 * w + 4 * j + (lane >> 4);
+      qraw[j] = row < a.lq ? *(const v4i*)(qb + row * a.q_st) : v4i{0, 0, 0, 0};
+    }
   }
 
   // DMA: wave w moves K rows (XK / 4) w .. + XK / 4 and V^T rows 32 w .. 32 w + 31 of a tile, 1 KB per
@@ -198,13 +202,28 @@ __global__ __launch_bounds__(XT, XOCC) void cross_attn_kernel(const uint16_t* __
     for (int i = 0; i < 16; ++i) o[mt][i] = 0.f;
   float m_ref = -INFINITY, l_run = 0.f;
 
+  issue(0, 0);   // tile 0's K / V travel with the Q rows
+  // Q^T B operand: lane (lq, hf) holds query 32 w + lq of the tile, channels 16 st + 8 hf .. + 8. The rows pass
+  // through the LDS after stage 0 (256-byte rows, chunk c at position c ^ (row & 15)), 8 KB a wave.
+  static_assert(XSTAGE + XWAVES * 32 * 256 <= XSTAGES * XSTAGE, "Q staging");
+  bf8 qf[8];
+  {
+    uint8_t* sq = xlds + XSTAGE + w * 32 * 256;
 #pragma unroll
-  for (int i = 0; i < XSTAGES - 1; ++i)
+    for (int j = 0; j < 8; ++j) {
+      const int r = 4 * j + (lane >> 4);
+      *(v4i*)(sq + r * 256 + ((c16 ^ (r & 15)) << 4)) = qraw[j];
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's rows are in LDS (it reads only its own)
+#pragma unroll
+    for (int st = 0; st < 8; ++st) qf[st] = as_bf8(*(const v4i*)(sq + lq * 256 + (((2 * st + hf) ^ (lq & 15)) << 4)));
+    asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]), "+v"(qf[6]),
+                 "+v"(qf[7]));
+  }
+  __syncthreads();   // every wave holds its fragments: the staging area is free for the next tiles' DMA
+#pragma unroll
+  for (int i = 1; i < XSTAGES - 1; ++i)
     if (i < ntile) issue(i, i);
-  // the Q fragments are complete before the loop (the compiler waits here, for the DMAs issued above as well:
-  // its own wait at the first product inside the loop would otherwise also wait for later tiles' DMAs)
-  asm volatile("" : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3]), "+v"(qf[4]), "+v"(qf[5]), "+v"(qf[6]),
-               "+v"(qf[7]));
 
   // one tile in stage S (a constant, so every LDS address is a register plus an immediate)
   auto tile = [&](int tl, auto stage) {
@@ -292,17 +311,29 @@ __global__ __launch_bounds__(XT, XOCC) void cross_attn_kernel(const uint16_t* __
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     l_run = __uint_as_float(r[0]) + __uint_as_float(r[1]);   // both halves of the query's keys
   }
-  if (qrow >= a.lq) return;
+  // O / l through LDS (rows of 272 bytes: the 16 rows a 16-lane group writes start 16 bytes apart in the banks),
+  // then out as whole rows: each store instruction writes 4 rows x 256 contiguous bytes
   const float inv_l = 1.f / l_run;
-  uint16_t* op = out + b * a.o_sb + qrow * a.o_st + h * a.o_sh;
+  constexpr int OROW = D * 2 + 16;
+  static_assert(XWAVES * 32 * OROW <= XSTAGES * XSTAGE, "O staging");
+  __syncthreads();   // every wave is done with the stages
+  uint8_t* so = xlds + w * 32 * OROW;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {   // channels 32 mt + 8 i + 4 hf + 0..3
-      const int ch = 32 * mt + 8 * i + 4 * hf;
-      *(uint2*)(op + ch) = make_uint2(pack_bf16(o[mt][4 * i] * inv_l, o[mt][4 * i + 1] * inv_l),
-                                      pack_bf16(o[mt][4 * i + 2] * inv_l, o[mt][4 * i + 3] * inv_l));
-    }
+    for (int i = 0; i < 4; ++i)   // channels 32 mt + 8 i + 4 hf + 0..3
+      *(uint2*)(so + lq * OROW + (32 * mt + 8 * i + 4 * hf) * 2) =
+          make_uint2(pack_bf16(o[mt][4 * i] * inv_l, o[mt][4 * i + 1] * inv_l),
+                     pack_bf16(o[mt][4 * i + 2] * inv_l, o[mt][4 * i + 3] * inv_l));
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's rows are in LDS (each wave reads only its own)
+  uint16_t* ob = out + b * a.o_sb + h * a.o_sh + c16 * 8;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = 4 * j + (lane >> 4);
+    const int64_t row = (int64_t)qt * XQ + 32 * w + r;
+    const v4i x = *(const v4i*)(so + r * OROW + c16 * 16);
+    if (row < a.lq) *(v4i*)(ob + row * a.o_st) = x;
+  }
 }
 
 }  // namespace lbw
