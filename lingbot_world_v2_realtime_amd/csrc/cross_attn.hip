@@ -225,40 +225,84 @@ __global__ __launch_bounds__(XT, XOCC) void cross_attn_kernel(const uint16_t* __
   for (int i = 1; i < XSTAGES - 1; ++i)
     if (i < ntile) issue(i, i);
 
-  // one tile in stage S (a constant, so every LDS address is a register plus an immediate)
-  auto tile = [&](int tl, auto stage) {
+  // The tiles go in pairs: both tiles' scores, one running-max update and O rescale for the 64 keys, then each
+  // tile's P V. Tile t sits in stage t % 3; a pair's first DMA (tile t0 + 2) goes into the stage of tile t0 - 1,
+  // its second (tile t0 + 3) into the first tile's stage once every wave's P V of it is done. Stages are
+  // constants, so every LDS address is a register plus an immediate.
+  static_assert(XK == 32 && XSTAGES == 3, "the pair schedule assumes three stages of 32 keys");
+  // S^T of the tile in stage S: lane (lq, hf) value i is key 8 (i >> 2) + 4 hf + (i & 3) of the tile
+  auto qk = [&](auto stage) {
     constexpr int S = decltype(stage)::value;
-    // this wave's pieces of tile tl have landed (those of the tiles after it may be in flight)
-    const int ahead = min(ntile - 1 - tl, XSTAGES - 2);
-    xwait_vm(ahead > 0 ? 2 * NDMA * ahead : 0);
-    __syncthreads();   // ... and every wave's; every wave is done with tile tl - 1's stage
-    if (tl + XSTAGES - 1 < ntile) issue(tl + XSTAGES - 1, (S + XSTAGES - 1) % XSTAGES);
     const uint8_t* sb = xlds + S * XSTAGE;
-    // S^T of keys 32 kt .. + 31: lane (lq, hf) value i is key 32 kt + 8 (i >> 2) + 4 hf + (i & 3)
-    v16f s[XKT];
+    v16f sc;
 #pragma unroll
-    for (int kt = 0; kt < XKT; ++kt) {
+    for (int i = 0; i < 16; ++i) sc[i] = 0.f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[kt][i] = 0.f;
-#pragma unroll
-      for (int st = 0; st < 8; ++st)
-        s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(*(const v4i*)(sb + kt * 32 * 256 + kro[st])),
-                                                        qf[st], s[kt], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);   // the phases stay apart: reads hoisted across them cost registers
-    if ((tl + 1) * XK > klen) {   // the ragged last tile: keys past klen drop out
+    for (int st = 0; st < 8; ++st)
+      sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(*(const v4i*)(sb + kro[st])), qf[st], sc, 0, 0, 0);
+    return sc;
+  };
+  auto mask = [&](v16f& sc, int tl) {   // the ragged last tile: keys past klen drop out
+    if ((tl + 1) * XK > klen) {
       const int kb = tl * XK + 4 * hf;
 #pragma unroll
-      for (int kt = 0; kt < XKT; ++kt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (kb + 32 * kt + 8 * (i >> 2) + (i & 3) >= klen) s[kt][i] = -INFINITY;
+      for (int i = 0; i < 16; ++i)
+        if (kb + 8 * (i >> 2) + (i & 3) >= klen) sc[i] = -INFINITY;
     }
-    float mx = -INFINITY;
+  };
+  // P^T fragment u: values i = 8 u .. 8 u + 7 = keys 16 u + {4 hf + 0..3, 8 + 4 hf + 0..3}; P = exp2(s sl2 - m)
+  // <= 1, on v_exp_f32 itself (exp2f adds a compare, a select and a v_ldexp per value to keep results below
+  // 2^-126 exact; weights that small do not matter next to the row's largest, exactly 1). Returns the sum of P.
+  auto probs = [&](const v16f& sc, float nm, v4i (&pf)[2]) {
+    float ps[2];
 #pragma unroll
-    for (int kt = 0; kt < XKT; ++kt)
+    for (int u = 0; u < 2; ++u) {
+      float p[8];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+      for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(sc[8 * u + j], a.sl2, nm));
+      ps[u] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+      pf[u] = v4i{(int)pack_bf16(p[0], p[1]), (int)pack_bf16(p[2], p[3]), (int)pack_bf16(p[4], p[5]),
+                  (int)pack_bf16(p[6], p[7])};
+    }
+    return ps[0] + ps[1];
+  };
+  // O^T += V^T P^T: A = V^T row 32 mt + lq, the lane's 8 keys of u: one 16-byte chunk (the prepared V^T stores
+  // each 16-key group in the fragment order)
+  auto pv = [&](auto stage, const v4i (&pf)[2]) {
+    constexpr int S = decltype(stage)::value;
+    const uint8_t* sb = xlds + S * XSTAGE;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const v4i vf = *(const v4i*)(sb + mt * 32 * (2 * XK) + vro[0][u]);
+        o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), as_bf8(pf[u]), o[mt], 0, 0, 0);
+      }
+  };
+  auto pair = [&](int t0, auto sa, auto sb) {
+    constexpr int SA = decltype(sa)::value, SB = decltype(sb)::value, SC = 3 - SA - SB;
+    const bool two = t0 + 1 < ntile;   // workgroup-uniform
+    xwait_vm(0);       // this wave's pieces of tiles t0 and t0 + 1 have landed
+    __syncthreads();   // ... and every wave's; every wave is done with tile t0 - 1's stage
+    if (t0 + 2 < ntile) issue(t0 + 2, SC);
+    v16f s0 = qk(ic<SA>{}), s1;
+    if (two) {
+      s1 = qk(ic<SB>{});
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s1[i] = -INFINITY;
+    }
+    __builtin_amdgcn_sched_barrier(0);   // the phases stay apart: reads hoisted across them cost registers
+    mask(s0, t0);
+    if (two) mask(s1, t0 + 1);
+    float m3[6];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) m3[i] = fmaxf(fmaxf(s0[3 * i], s0[3 * i + 1]), s0[3 * i + 2]);
+    m3[5] = fmaxf(s0[15], s1[15]);
+    float mx = fmaxf(fmaxf(m3[0], m3[1]), fmaxf(m3[2], m3[3]));
+    mx = fmaxf(mx, fmaxf(m3[4], m3[5]));
+#pragma unroll
+    for (int i = 0; i < 5; ++i) mx = fmaxf(mx, fmaxf(fmaxf(s1[3 * i], s1[3 * i + 1]), s1[3 * i + 2]));
     mx = max_xor32(mx) * a.sl2;   // exp2 domain; finite: every tile holds a valid key
     // the exact running max: the row's largest P is exactly 1, which keeps its bf16 rounding error at zero (a
     // reference max that moves only by steps measured 19 % more mean error on a peaked softmax)
@@ -269,43 +313,20 @@ __global__ __launch_bounds__(XT, XOCC) void cross_attn_kernel(const uint16_t* __
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[mt][i] *= alpha;
     m_ref = m_new;
-    // P^T fragments (kt, u): values i = 8 u .. 8 u + 7 = keys 32 kt + 16 u + {4 hf + 0..3, 8 + 4 hf + 0..3};
-    // P = exp2(s sl2 - m) <= 1, on v_exp_f32 itself (exp2f adds a compare, a select and a v_ldexp per value to
-    // keep results below 2^-126 exact; weights that small do not matter next to the row's largest, exactly 1)
-    const float nm = -m_ref;
-    v4i pf[XKT][2];
-    float ps[XKT][2];
-#pragma unroll
-    for (int kt = 0; kt < XKT; ++kt)
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        float p[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(fmaf(s[kt][8 * u + j], a.sl2, nm));
-        ps[kt][u] = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        pf[kt][u] = v4i{(int)pack_bf16(p[0], p[1]), (int)pack_bf16(p[2], p[3]), (int)pack_bf16(p[4], p[5]),
-                        (int)pack_bf16(p[6], p[7])};
-      }
-    float lt = ps[0][0] + ps[0][1];
-    if (XKT > 1) lt += ps[XKT - 1][0] + ps[XKT - 1][1];
+    v4i pf0[2], pf1[2];
+    float lt = probs(s0, -m_ref, pf0);
+    if (two) lt += probs(s1, -m_ref, pf1);
     l_run = fmaf(l_run, alpha, lt);
     __builtin_amdgcn_sched_barrier(0);
-    // O^T += V^T P^T: A = V^T row 32 mt + lq, the lane's 8 keys of (kt, u): one 16-byte chunk (the prepared
-    // V^T stores each 16-key group in the fragment order)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int kt = 0; kt < XKT; ++kt)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const v4i vf = *(const v4i*)(sb + mt * 32 * (2 * XK) + vro[kt][u]);
-          o[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf8(vf), as_bf8(pf[kt][u]), o[mt], 0, 0, 0);
-        }
+    pv(ic<SA>{}, pf0);
+    __syncthreads();   // every wave is done with tile t0's stage
+    if (t0 + 3 < ntile) issue(t0 + 3, SA);
+    if (two) pv(ic<SB>{}, pf1);
   };
-  for (int tl = 0; tl < ntile; tl += XSTAGES) {
-    tile(tl, ic<0>{});
-    if (tl + 1 < ntile) tile(tl + 1, ic<1>{});
-    if (XSTAGES > 2 && tl + 2 < ntile) tile(tl + 2, ic<(XSTAGES > 2 ? 2 : 0)>{});
+  for (int t0 = 0; t0 < ntile; t0 += 6) {
+    pair(t0, ic<0>{}, ic<1>{});
+    if (t0 + 2 < ntile) pair(t0 + 2, ic<2>{}, ic<0>{});
+    if (t0 + 4 < ntile) pair(t0 + 4, ic<1>{}, ic<2>{});
   }
   {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
