@@ -180,18 +180,20 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
 
-__device__ __forceinline__ void dma16(const void* src, uint8_t* lds) {
+// The source is a wave-uniform base plus a 32-bit per-lane byte offset (the global instruction's scalar-base form:
+// no 64-bit address per lane to form).
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint8_t* lds) {
   uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
                "s_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(src), "s"(lds_addr(lds)) : "memory");
+               : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
 }
 
-__device__ __forceinline__ void dma4(const void* src, uint8_t* lds) {
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint8_t* lds) {
   uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\t"
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\t"
                "s_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(src), "s"(lds_addr(lds)) : "memory");
+               : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
@@ -261,10 +263,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   seek(lc, lb);
   auto issue = [&](int stage) {
     uint8_t* sb = lds + stage * ST_BYTES + w * 1024;
-    dma16(kbase + koff, sb + ST_K);
-    dma16(vbase + voff, sb + ST_V);
-    if (TWO) dma16(vlbase + voff, sb + ST_VLO);
-    if (lane == 0) dma4(ksbase, lds + TAB_KS + (stage * AT_WAVES + w) * 4);   // one lane: 4 bytes
+    dma16(kbase, (uint32_t)koff, sb + ST_K);
+    dma16(vbase, (uint32_t)voff, sb + ST_V);
+    if (TWO) dma16(vlbase, (uint32_t)voff, sb + ST_VLO);
+    if (lane == 0) dma4(ksbase, 0u, lds + TAB_KS + (stage * AT_WAVES + w) * 4);   // one lane: 4 bytes
   };
   auto advance = [&]() {
     if (--lrem == 0) {
