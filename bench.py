@@ -347,12 +347,14 @@ DIM, FFN = 1536, 8960       # the DiT's model and feed-forward widths
 def fp8_linear_calls(dev, steps=30):
     """The DiT's FP8 linears at the chunk shape (6032 tokens): q/k/v/o (1536 -> 1536) and the two feed-forward
     layers (1536 -> 8960, 8960 -> 1536). Per call: the activation quantisation (lbw_quant_rows_fp8) and
-    hipBLASLt's rowwise-scaled FP8 GEMM with the bias. Flops 2 M K N against 5.0 PFLOP/s dense fp8.
+    hipBLASLt's rowwise-scaled FP8 GEMM with the bias, timed with hipBLASLt's default solution and with the tuned
+    solution table (`ms` is the latter when the table was read). Flops 2 M K N against 5.0 PFLOP/s dense fp8.
     act_quant_call_ms times the quantisation call alone from Python; at ~6-9 us of kernel time it is bound by the
     launch path, so it is an upper bound on the kernel."""
     import torch
     from lingbot_world_v2_realtime_amd import kernels
-    from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear
+    import torch.cuda.tunable as tunable
+    from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear, use_tuned_gemms
     out = {}
     stream = torch.cuda.current_stream(dev)
     for name, (k, n) in (("proj_1536x1536", (DIM, DIM)), ("ffn_up_1536x8960", (DIM, FFN)),
@@ -360,14 +362,22 @@ def fp8_linear_calls(dev, steps=30):
         lin = torch.nn.Linear(k, n).to(torch.bfloat16).to(dev)
         f = FP8Linear(lin)
         x = torch.randn(1, LQ, k, device=dev).to(torch.bfloat16)
-        for _ in range(3):
-            f(x)
-        torch.cuda.synchronize()
-        ms = _timed(lambda: f(x), steps, stream)
+        times = {}
+        # hipBLASLt's default solution, then with the tuned-solution table (layers/fp8_gemm_solutions.csv)
+        for mode in ("default", "table"):
+            table = use_tuned_gemms() if mode == "table" else False
+            for _ in range(3):
+                f(x)
+            torch.cuda.synchronize()
+            times[mode] = _timed(lambda: f(x), steps, stream)
+            if mode == "table":
+                tunable.enable(False)
+        ms = times["table"] if table else times["default"]
         q_ms = _timed(lambda: kernels.quant_rows_fp8(x.view(LQ, k)), steps, stream)
         flops = 2.0 * LQ * k * n
         tf = flops / (ms * 1e-3) / 1e12
-        out[name] = {"ms": round(ms, 4), "act_quant_call_ms": round(q_ms, 4), "TFLOP/s": round(tf, 1),
+        out[name] = {"ms": round(ms, 4), "default_solution_ms": round(times["default"], 4), "gemm_table": table,
+                     "act_quant_call_ms": round(q_ms, 4), "TFLOP/s": round(tf, 1),
                      "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
     # the MXFP8 mode (per-32 E8M0 scales) at the projection shape: its GEMM pads the rows to 128
     from lingbot_world_v2_realtime_amd.layers.linear import MXFP8Linear

@@ -5,12 +5,55 @@ scale per 32 values along K for both; the GEMM accumulates in fp32 and writes bf
 On MI355X the per-row quantisation of weights and activations is a HIP kernel (lbw_quant_rows_fp8, bit for bit the
 reference's formula) and the GEMM is hipBLASLt's rowwise-scaled FP8 GEMM, reached through torch._scaled_mm with the
 bias in its epilogue -- a plain library GEMM, which the dense FP8 MFMA path of the library already serves well.
+For the shapes in fp8_gemm_solutions.csv, use_tuned_gemms() makes the GEMM take the hipBLASLt solution measured
+fastest for that shape instead of the library's default pick (tune_gemms() writes such a table).
 """
+import os
+
 import torch
 
 from .. import kernels
 
-__all__ = ["FP8Linear", "MXFP8Linear", "convert_to_fp8"]
+__all__ = ["FP8Linear", "MXFP8Linear", "convert_to_fp8", "use_tuned_gemms", "tune_gemms", "GEMM_TABLE"]
+
+# hipBLASLt solutions for the DiT's rowwise FP8 GEMMs at the chunk shape (6032 tokens), as a TunableOp results file:
+# a key per (layout, N, M, K, leading dims, rowwise scales, bias type), the solution, its measured time, and the
+# torch / HIP / hipBLASLt versions and GPU it holds for. Only the 8960 -> 1536 feed-forward projection is listed:
+# its tuned solution runs in 74-76 us against 96-97 us for the default pick; for 1536 -> 1536 and 1536 -> 8960 the
+# tuned solutions were no faster in use (27.8 vs 26.6 us, 105.4 vs 105.2 us), so those keep the default.
+GEMM_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "fp8_gemm_solutions.csv")
+
+
+def use_tuned_gemms(path=GEMM_TABLE):
+    """Make torch._scaled_mm take the solution `path` records for each GEMM shape in it (torch's TunableOp, read
+    only: nothing is measured or written). Other shapes keep hipBLASLt's default; a table recorded with other
+    library versions or on another GPU is rejected by TunableOp's validators. Process-wide. Returns whether the
+    table was read."""
+    import torch.cuda.tunable as tunable
+    tunable.enable(True)
+    tunable.tuning_enable(False)
+    tunable.record_untuned_enable(False)
+    return bool(tunable.read_file(path))
+
+
+def tune_gemms(shapes, path, device="cuda", bias=True):
+    """Measure hipBLASLt's solutions for rowwise FP8 GEMMs of the given (M, K, N) shapes (an [M, K] activation times
+    the [N, K] weight of an FP8Linear, bf16 out, with a bf16 bias when `bias`) and write the fastest of each into
+    the TunableOp results file `path`. Tuning stays on for the process afterwards; read the table back with
+    use_tuned_gemms() in the process that runs the model. TunableOp writes the file (by the time the process ends)."""
+    import torch.cuda.tunable as tunable
+    tunable.enable(True)
+    tunable.tuning_enable(True)
+    tunable.set_filename(path)
+    for m, k, n in shapes:
+        x8 = torch.randn(m, k, device=device).to(torch.float8_e4m3fn)
+        w8 = torch.randn(n, k, device=device).to(torch.float8_e4m3fn)
+        xs = torch.ones(m, 1, device=device)
+        ws = torch.ones(1, n, device=device)
+        b = torch.zeros(n, device=device, dtype=torch.bfloat16) if bias else None
+        torch._scaled_mm(x8, w8.t(), scale_a=xs, scale_b=ws, bias=b, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    return tunable.get_results()
 
 
 class FP8Linear(torch.nn.Module):

@@ -76,6 +76,39 @@ def test_fp8_linear(m, k, n, bias):
     assert rel < 6e-2
 
 
+def test_fp8_linear_tuned_table():
+    """The tuned-solution table (layers/fp8_gemm_solutions.csv) is accepted on this GPU and library version, and
+    the shape it covers, the feed-forward down projection 6032 x 8960 -> 1536 with its bias, gives the same-operand
+    fp32 result to the tolerance of the default solution."""
+    import torch.cuda.tunable as tunable
+    from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear, use_tuned_gemms
+    m, k, n = 6032, 8960, 1536
+    g = torch.Generator().manual_seed(7)
+    lin = torch.nn.Linear(k, n).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(n, k, generator=g) * 0.02)
+        lin.bias.copy_(torch.randn(n, generator=g) * 0.1)
+    lin = lin.to(DEV)
+    f = FP8Linear(lin)
+    x = torch.randn(1, m, k, generator=g).to(torch.bfloat16)
+    y0 = f(x.to(DEV))
+    try:
+        assert use_tuned_gemms()
+        y = f(x.to(DEV))
+        torch.cuda.synchronize()
+    finally:
+        tunable.enable(False)
+    xb, xs = fp8.quant_rows(x.reshape(-1, k))
+    wb, ws = fp8.quant_rows(lin.weight.detach().cpu())
+    ref = fp8.dequant_rows(xb, xs) @ fp8.dequant_rows(wb, ws).t() + lin.bias.detach().cpu().to(torch.bfloat16).float()
+    scale = ref.abs().max().item()
+    e = (y.reshape(-1, n).float().cpu() - ref).abs().max().item()
+    e0 = (y0.reshape(-1, n).float().cpu() - ref).abs().max().item()
+    record(f"FP8Linear {m}x{k}x{n} with the tuned solution: vs same-operand fp32 max {e:.2e} (default solution "
+           f"{e0:.2e}; |ref| max {scale:.2e})")
+    assert e <= 1e-2 * scale
+
+
 def test_convert_to_fp8_selection():
     from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear, convert_to_fp8
     blk = torch.nn.Sequential(torch.nn.Linear(1536, 1536), torch.nn.Sequential(torch.nn.Linear(1536, 8960)),
