@@ -3,9 +3,11 @@
 // output row) and its activations (every call, per token). The GEMM itself is a plain rowwise-scaled FP8 GEMM
 // (hipBLASLt); this kernel is the part around it that runs on every call.
 //
-// One workgroup per row: 256 threads, 16-byte loads; the amax pass and the quantise pass read the row twice (the
-// second read comes from the cache: a row is a few KB).
+// One workgroup per row: 256 threads, 16-byte loads. Rows of up to 16384 values stay in registers between the
+// amax and the quantisation (one read); longer rows are read twice (the second read from the cache).
 #include "lbw_common.h"
+
+#pragma clang fp contract(off)
 
 namespace lbw {
 
@@ -28,9 +30,83 @@ struct Row8<float> {      // fp32: 8 values = 32 bytes
   }
 };
 
-template <typename T>
+// x / sc rounded to nearest, from the row's reciprocal r = RN(1 / sc): q = RN(x r) is within an ulp of x / sc, the
+// remainder x - q sc is exact under an FMA, and RN(q + rem r) is the correctly rounded quotient (Markstein's
+// correction step); the sign comes from x, so a zero quotient keeps it. Equal to IEEE division wherever
+// |x / sc| >= 2^-12 (a smaller quotient is +-0 in e4m3 either way): tests/test_fp8_division.py checks every bf16 x
+// against 2048 scales and 2e7 random fp32 pairs (2e9 pairs and 2e4 scales checked once as well). Three
+// instructions against ~10 for the division.
+__device__ __forceinline__ float div_sc(float x, float sc, float r) {
+  const float q = x * r;
+  return __builtin_copysignf(fmaf(fmaf(-q, sc, x), r, q), x);
+}
+
+// e4m3 of 8 values divided by the row scale, as 8 bytes; x / scale is within 448 up to its own rounding, and the
+// clamp keeps a rounding above 448 off the overflow path
+__device__ __forceinline__ uint2 quant8(const float* f, float sc, float r) {
+  uint32_t w[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const float y0 = fminf(fmaxf(div_sc(f[4 * h], sc, r), -FP8_MAX), FP8_MAX);
+    const float y1 = fminf(fmaxf(div_sc(f[4 * h + 1], sc, r), -FP8_MAX), FP8_MAX);
+    const float y2 = fminf(fmaxf(div_sc(f[4 * h + 2], sc, r), -FP8_MAX), FP8_MAX);
+    const float y3 = fminf(fmaxf(div_sc(f[4 * h + 3], sc, r), -FP8_MAX), FP8_MAX);
+    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+    pk = __builtin_amdgcn_cvt_pk_fp8_f32(y2, y3, pk, true);
+    w[h] = (uint32_t)pk;
+  }
+  return make_uint2(w[0], w[1]);
+}
+
+// the row's amax over the workgroup (in every thread) -> its scale, written by thread 0
+__device__ __forceinline__ float row_scale(float amax, float* s_red, float* scale, int64_t row) {
+  const int t = threadIdx.x;
+  amax = wave_max(amax);
+  if ((t & 63) == 0) s_red[t >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float sc = fmaxf(__fdiv_rn(amax, FP8_MAX), FP8_SCALE_FLOOR);
+  if (t == 0) scale[row] = sc;
+  return sc;
+}
+
+// Rows of at most NCH * 2048 values: thread t holds 8-value chunks t, t + 256, ... in registers.
+template <typename T, int NCH>
 __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict__ x, int64_t cols, int64_t s_row,
                                                              uint8_t* __restrict__ x8, float* __restrict__ scale) {
+  __shared__ float s_red[4];
+  const int64_t row = blockIdx.x;
+  const T* xr = x + row * s_row;
+  const int t = threadIdx.x;
+  float f[NCH][8];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = 8 * (int64_t)(t + 256 * i);
+    if (c < cols) {
+      Row8<T>::load(xr + c, f[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[i][e]));
+  }
+  const float sc = row_scale(amax, s_red, scale, row);
+  const float r = __fdiv_rn(1.f, sc);
+  uint8_t* outr = x8 + row * cols;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = 8 * (int64_t)(t + 256 * i);
+    if (c < cols) *(uint2*)(outr + c) = quant8(f[i], sc, r);
+  }
+}
+
+// Longer rows: the amax pass and the quantise pass each read the row.
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rows_fp8_long_kernel(const T* __restrict__ x, int64_t cols,
+                                                                  int64_t s_row, uint8_t* __restrict__ x8,
+                                                                  float* __restrict__ scale) {
   __shared__ float s_red[4];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * s_row;
@@ -42,27 +118,33 @@ __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
   }
-  amax = wave_max(amax);
-  if ((t & 63) == 0) s_red[t >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  const float sc = fmaxf(__fdiv_rn(amax, FP8_MAX), FP8_SCALE_FLOOR);
-  if (t == 0) scale[row] = sc;
+  const float sc = row_scale(amax, s_red, scale, row);
+  const float r = __fdiv_rn(1.f, sc);
   uint8_t* outr = x8 + row * cols;
   for (int64_t c = 8 * (int64_t)t; c < cols; c += 8 * 256) {
     float f[8];
     Row8<T>::load(xr + c, f);
-    uint32_t w[2] = {0, 0};
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      // x / scale is within 448 up to its own rounding; the clamp keeps a rounding above 448 off the overflow path
-      const float y0 = fminf(fmaxf(__fdiv_rn(f[e], sc), -FP8_MAX), FP8_MAX);
-      const float y1 = fminf(fmaxf(__fdiv_rn(f[e + 1], sc), -FP8_MAX), FP8_MAX);
-      const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false) & 0xFFFFu;
-      w[e >> 2] |= pk << (16 * ((e >> 1) & 1));
-    }
-    *(uint2*)(outr + c) = make_uint2(w[0], w[1]);
+    *(uint2*)(outr + c) = quant8(f, sc, r);
   }
+}
+
+template <typename T>
+static void launch_quant_rows(const T* x, int64_t rows, int64_t cols, int64_t s_row, uint8_t* x8, float* scale,
+                              hipStream_t stream) {
+  const dim3 grid((unsigned)rows), block(256);
+  const int64_t nch = (cols + 2047) / 2048;
+  if (nch <= 1)
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 1>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+  else if (nch <= 2)
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 2>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+  else if (nch <= 4)
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 4>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+  else if (nch <= 5)
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 5>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+  else if (nch <= 8)
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 8>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+  else
+    hipLaunchKernelGGL(quant_rows_fp8_long_kernel<T>, grid, block, 0, stream, x, cols, s_row, x8, scale);
 }
 
 // MXFP8 (the reference's MXFP8Linear, lingbot/layers/linear.py:42-50): per 32 consecutive values of a row,
@@ -138,11 +220,9 @@ extern "C" int lbw_quant_rows_fp8(const void* x, int x_is_fp32, int64_t rows, in
   if (s_row % 8 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)x8 & 7)) return LBW_E_ALIGN;
   if (const int dv = check_device()) return dv;
   if (x_is_fp32)
-    hipLaunchKernelGGL(quant_rows_fp8_kernel<float>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
-                       (const float*)x, cols, s_row, x8, scale);
+    launch_quant_rows((const float*)x, rows, cols, s_row, x8, scale, (hipStream_t)stream);
   else
-    hipLaunchKernelGGL(quant_rows_fp8_kernel<uint16_t>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
-                       (const uint16_t*)x, cols, s_row, x8, scale);
+    launch_quant_rows((const uint16_t*)x, rows, cols, s_row, x8, scale, (hipStream_t)stream);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }

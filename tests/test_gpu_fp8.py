@@ -19,7 +19,9 @@ def _k():
 
 @pytest.mark.parametrize("rows,cols,dtype", [(1, 16, torch.bfloat16), (37, 1536, torch.bfloat16),
                                              (6032, 1536, torch.bfloat16), (100, 8960, torch.bfloat16),
-                                             (1536, 1536, torch.float32), (3, 2064, torch.float32)])
+                                             (1536, 1536, torch.float32), (3, 2064, torch.float32),
+                                             (9, 4112, torch.bfloat16), (20, 12288, torch.float32),
+                                             (64, 16400, torch.bfloat16)])
 def test_quant_rows_bit_exact(rows, cols, dtype):
     g = torch.Generator().manual_seed(rows + cols)
     x = (torch.randn(rows, cols, generator=g) * torch.exp(torch.randn(rows, 1, generator=g) * 2)).to(dtype)
@@ -29,6 +31,21 @@ def test_quant_rows_bit_exact(rows, cols, dtype):
     rb, rs = fp8.quant_rows(x)
     assert torch.equal(x8.view(torch.uint8).cpu(), rb)
     assert torch.equal(sc.cpu(), rs)
+
+
+def test_quant_rows_signed_zero_and_subnormal_edge():
+    """Signed zeros keep their sign and quotients around e4m3's smallest subnormals (2^-9, ties at odd multiples of
+    2^-10) round as the reference's division does: row amax 448 makes the scale exactly 1."""
+    edge = [0.0, -0.0, 2 ** -10, -2 ** -10, 1.5 * 2 ** -10, 2 ** -9, 3 * 2 ** -10, 2 ** -11, 2 ** -6, 448.0, -448.0,
+            0.3, -1e-30, 1e-30, 5 * 2 ** -10, -7 * 2 ** -10]
+    for dtype in (torch.bfloat16, torch.float32):
+        x = torch.tensor(edge * 2, dtype=torch.float32).reshape(2, -1).to(dtype)
+        x[1] *= 3.0 ** 0.5                                   # a scale that is not a power of two
+        x8, sc = _k().quant_rows_fp8(x.to(DEV))
+        torch.cuda.synchronize()
+        rb, rs = fp8.quant_rows(x)
+        assert torch.equal(x8.view(torch.uint8).cpu(), rb) and torch.equal(sc.cpu(), rs), dtype
+        assert int(rb[0, 1]) == 0x80                          # -0 stays -0
 
 
 def test_quant_rows_strided_view():
