@@ -132,7 +132,8 @@ int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, int64_t batch
 /*
  * The cross-attention context in the layout lbw_cross_attn_fwd reads: k, v [batch][lk][heads][128] bf16 (strides
  * *_s_batch, *_s_tok, *_s_head) -> k_prep [batch * heads][Lkp][128] and vt_prep [batch * heads][128][Lkp] (V
- * transposed), Lkp = ceil64(lk), padding keys zero. The reference computes the cross-attention K / V once per
+ * transposed; within each 16-key group the keys are stored in the order 0-3, 8-11, 4-7, 12-15), Lkp = ceil64(lk),
+ * padding keys zero. The reference computes the cross-attention K / V once per
  * generation and keeps them (crossattn_cache, lingbot/models/lingbot_world/transformer.py:251-266); this is the
  * one-time step that goes with it.
  */
