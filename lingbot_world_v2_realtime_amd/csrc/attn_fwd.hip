@@ -180,13 +180,31 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
 
-// The source is a wave-uniform base plus a 32-bit per-lane byte offset (the global instruction's scalar-base form:
+// A block's tiles (K, V and, with TWO, the V residual) in one asm, M0 saved once and restored once around the loads.
+// Each source is a wave-uniform base plus a 32-bit per-lane byte offset (the global instruction's scalar-base form:
 // no 64-bit address per lane to form).
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint8_t* lds) {
+template <bool TWO>
+__device__ __forceinline__ void dma16_tiles(const void* kb, uint32_t koff, const void* vb, const void* vlb, uint32_t voff,
+                                            uint8_t* lk, uint8_t* lv, uint8_t* lvl) {
   uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
-               "s_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
+  if (TWO)
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %5\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %3, %4\n\t"
+                 "s_mov_b32 m0, %8\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %3, %7\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv)), "s"(vlb),
+                   "s"(lds_addr(lvl))
+                 : "memory");
+  else
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %5\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %3, %4\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(keep)
+                 : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv))
+                 : "memory");
 }
 
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint8_t* lds) {
@@ -263,9 +281,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   seek(lc, lb);
   auto issue = [&](int stage) {
     uint8_t* sb = lds + stage * ST_BYTES + w * 1024;
-    dma16(kbase, (uint32_t)koff, sb + ST_K);
-    dma16(vbase, (uint32_t)voff, sb + ST_V);
-    if (TWO) dma16(vlbase, (uint32_t)voff, sb + ST_VLO);
+    dma16_tiles<TWO>(kbase, (uint32_t)koff, vbase, TWO ? (const void*)vlbase : nullptr, (uint32_t)voff, sb + ST_K,
+                     sb + ST_V, sb + ST_VLO);
     if (lane == 0) dma4(ksbase, 0u, lds + TAB_KS + (stage * AT_WAVES + w) * 4);   // one lane: 4 bytes
   };
   auto advance = [&]() {
