@@ -207,6 +207,7 @@ __device__ __forceinline__ void dma16_tiles(const void* kb, uint32_t koff, const
                  : "memory");
 }
 
+// 4 bytes per active lane (the block's K scale, issued by one lane)
 __device__ __forceinline__ void dma4(const void* base, uint32_t off, uint8_t* lds) {
   uint32_t keep;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\t"
