@@ -169,6 +169,22 @@ def test_attention_small_vs_oracle(lq, lk):
     assert err_sdpa.mean() <= 1.1 * err_scheme.mean() + 1e-5
 
 
+@pytest.mark.parametrize("lk", [65000, 66000])
+def test_attention_long_window(lk):
+    """One chunk of 65000 / 66000 keys (1016 / 1032 key blocks, over a thousand passes of the block loop per tile)
+    for 64 queries: the kernel matches the oracle as at the DiT's sizes."""
+    q, k, v, _ = emu.make_inputs(64, lk, h=1, seed=lk)
+    out = _attn_gpu(q, k, v)
+    ref = emu.attention(q, [emu.requant(k, v)], schedule_gx=_gx())[None]
+    sd = emu.sdpa_fp32(q, k, v)[None]
+    err_emu, err_sdpa, err_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    print(f"lk={lk} vs-emu max {err_emu.max():.3e} mean {err_emu.mean():.3e} | vs-sdpa mean {err_sdpa.mean():.3e} | "
+          f"emu vs-sdpa mean {err_scheme.mean():.3e}")
+    assert err_emu.mean() <= 0.1 * err_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert err_sdpa.max() <= 2 * err_scheme.max() + 1e-3
+    assert err_sdpa.mean() <= 1.1 * err_scheme.mean() + 1e-5
+
+
 def test_split_tiles_every_piece():
     """36 query tiles (6 heads x 1508 queries) over 8 XCDs: each XCD has fewer tiles than workgroups, so every
     tile's 24 key blocks are cut into pieces of several workgroups (at 32 workgroups per XCD, pieces of 1-4
