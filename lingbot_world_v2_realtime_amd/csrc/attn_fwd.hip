@@ -17,6 +17,7 @@
 // workgroup. A piece that is not a whole tile leaves an unnormalised partial (O, running max, row sum) in the
 // workspace, and attn_merge_kernel combines the pieces of each split tile.
 #include <atomic>
+#include <type_traits>
 
 #include "lbw_common.h"
 
@@ -286,14 +287,15 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
                      sb + ST_V, sb + ST_VLO);
     if (lane == 0) dma4(ksbase, 0u, lds + TAB_KS + (stage * AT_WAVES + w) * 4);   // one lane: 4 bytes
   };
-  auto advance = [&]() {
-    if (--lrem == 0) {
+  auto advance = [&](auto fast) {   // fast: the next block is in the same chunk (lrem >= 2)
+    if (!decltype(fast)::value && --lrem == 0) {
       ++lc;
       if (lc < a.n_seg) {
         seek(lc, 0);
         lrem = a.seg_blk0[lc + 1] - a.seg_blk0[lc];
       }
     } else {
+      if (decltype(fast)::value) --lrem;
       kbase += TILE_BYTES;
       vbase += TILE_BYTES;
       if (TWO) vlbase += TILE_BYTES;
@@ -330,7 +332,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   const int npre = n < LEAD ? n : LEAD;
   for (int i = 0; i < npre; ++i) {
     issue(i);
-    advance();
+    advance(std::false_type{});
   }
   float beta = 0.f;
   if (multi) {
@@ -357,7 +359,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
 
   v8i pb = {0, 0, 0, 0, 0, 0, 0, 0};
   int stage = 0, pstage = 0;
-  for (int it = 0;; ++it) {
+  int it = 0;
+  // One pass: the MFMA phase of block it and the softmax phase of block it. The fast form assumes what holds for
+  // most passes: the loader's block it + LEAD exists and lies in the loader's current chunk, and block it is
+  // neither the first nor the last block of its chunk (so no rescale to a new V scale, no key mask, no chunk
+  // step). It returns true after the last MFMA phase (it == n).
+  auto pass = [&](auto fast) -> bool {
+    constexpr bool FAST = decltype(fast)::value;
     // ---- MFMA phase: S of block it, P V of block it - 1 ----
     __builtin_amdgcn_s_setprio(1);
     // LDS reads run ahead of the MFMAs that consume them: all eight K fragments and the first two V fragments
@@ -414,9 +422,9 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     // phase, where the wave mostly waits for the matrix core (the softmax phase slows down with it), and after
     // the first two QK MFMAs, so the matrix core starts at once and the issue hides under their execution
     // (-1 to -2 % against issuing it before them, same-box A/B)
-    if (it + LEAD < n) {
+    if (FAST || it + LEAD < n) {
       issue(ldstage);
-      advance();
+      advance(fast);
       ldstage = ldstage + 1 == NSTAGE ? 0 : ldstage + 1;
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -450,9 +458,9 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       asm volatile("" : "+v"(st.o[0]), "+v"(st.o[1]), "+v"(st.o[2]), "+v"(st.o[3]));   // as for acc
     }
     __builtin_amdgcn_s_setprio(0);
-    if (it == n) break;
+    if (!FAST && it == n) return true;
     if (!grp_a) {   // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD in flight)
-      if (it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
+      if (FAST || it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
         wait_vm(NPB * (LEAD - 1));
       } else {
         const int ahead = n - 1 - (it + 1);
@@ -462,7 +470,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     phase_barrier();
 
     // ---- softmax phase for block it (chunk c) ----
-    if (c != c_prev) {
+    if (!FAST && c != c_prev) {
       // a new chunk (c_prev == c - 1: every chunk has a block): O (blocks before this one) to its V scale,
       // and its logit bias, both from the piece's LDS tables
       const float* rt = ratio_tab + c * D + 4 * g;
@@ -485,8 +493,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) si[16 * mt + i] = acc[mt][i];
-    const int valid = crem == 1 ? last_valid : KB;   // keys of this block that exist (>= 1)
-    if (valid < KB) {
+    const int valid = FAST || crem != 1 ? KB : last_valid;   // keys of this block that exist (>= 1)
+    if (!FAST && valid < KB) {
       const int vt = valid - 4 * g;   // key 32 mt + 8 (i >> 2) + 4 g + (i & 3) is past the end iff its
 #pragma unroll                        // lane-independent part reaches vt
       for (int i = 0; i < 32; ++i)
@@ -520,13 +528,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       pb[r] = wd;
     }
     // next block of the compute cursor
-    if (--crem == 0 && c + 1 < a.n_seg) {
+    if (--crem == 0 && !FAST && c + 1 < a.n_seg) {
       ++c;
       crem = a.seg_blk0[c + 1] - a.seg_blk0[c];
       last_valid = a.seg_len[c] - (crem - 1) * KB;
     }
     if (grp_a) {   // A's pieces of block it + 1 have landed (blocks up to it + LEAD may still be in flight)
-      if (it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
+      if (FAST || it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
         wait_vm(NPB * (LEAD - 1));
       } else {
         const int ahead = n - 1 - (it + 1);
@@ -536,6 +544,18 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     phase_barrier();
     pstage = stage;
     stage = stage + 1 == NSTAGE ? 0 : stage + 1;
+    ++it;
+    return false;
+  };
+  for (;;) {
+    // passes from here on that take the fast form: the loader stays in its chunk for f more blocks, block it is
+    // not its chunk's first (c == c_prev) and none of the f blocks is its chunk's last, and block it + f - 1 + LEAD
+    // still exists
+    int f = (lrem < crem ? lrem : crem) - 1;
+    if (n - LEAD - it < f) f = n - LEAD - it;
+    if (c != c_prev) f = 0;
+    for (; f > 0; --f) pass(std::true_type{});
+    if (pass(std::false_type{})) break;
   }
   if (grp_a) phase_barrier();   // matches group B's extra barrier at the start
   phase_barrier();               // every wave is done with the stages before they are refilled
