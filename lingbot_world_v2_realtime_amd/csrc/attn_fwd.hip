@@ -288,14 +288,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     if (lane == 0) dma4(ksbase, 0u, lds + TAB_KS + (stage * AT_WAVES + w) * 4);   // one lane: 4 bytes
   };
   auto advance = [&](auto fast) {   // fast: the next block is in the same chunk (lrem >= 2)
-    if (!decltype(fast)::value && --lrem == 0) {
+    if (!decltype(fast)::value && --lrem == 0) {   // the fast form's steps are taken off lrem after the run
       ++lc;
       if (lc < a.n_seg) {
         seek(lc, 0);
         lrem = a.seg_blk0[lc + 1] - a.seg_blk0[lc];
       }
     } else {
-      if (decltype(fast)::value) --lrem;
       kbase += TILE_BYTES;
       vbase += TILE_BYTES;
       if (TWO) vlbase += TILE_BYTES;
@@ -459,7 +458,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     }
     __builtin_amdgcn_s_setprio(0);
     if (!FAST && it == n) return true;
-    if (!grp_a) {   // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD in flight)
+    // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD in flight). The fast
+    // form waits in both groups (no branch): A's pieces of block it + 1 were issued LEAD - 1 passes ago, and A
+    // needs them by the end of this pass anyway.
+    if (FAST || !grp_a) {
       if (FAST || it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
         wait_vm(NPB * (LEAD - 1));
       } else {
@@ -504,7 +506,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     const int mx = halves_max_i(max32i(si));
     const float m_blk = (__int_as_float(mx) - S_MAGIC_F) * cb + beta;
     const bool moved = m_blk > m_ref + RESCALE_SLACK;
-    if (__any(moved)) {   // wave-uniform and rare
+    if (__builtin_expect(__any(moved), 0)) {   // wave-uniform and rare
       const float m_new = moved ? m_blk : m_ref;
       const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
       l_run *= alpha;
@@ -528,12 +530,12 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       pb[r] = wd;
     }
     // next block of the compute cursor
-    if (--crem == 0 && !FAST && c + 1 < a.n_seg) {
+    if (!FAST && --crem == 0 && c + 1 < a.n_seg) {   // the fast form's steps are taken off crem after the run
       ++c;
       crem = a.seg_blk0[c + 1] - a.seg_blk0[c];
       last_valid = a.seg_len[c] - (crem - 1) * KB;
     }
-    if (grp_a) {   // A's pieces of block it + 1 have landed (blocks up to it + LEAD may still be in flight)
+    if (FAST || grp_a) {   // A's pieces of block it + 1 have landed (blocks up to it + LEAD may still be in flight)
       if (FAST || it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
         wait_vm(NPB * (LEAD - 1));
       } else {
@@ -544,7 +546,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     phase_barrier();
     pstage = stage;
     stage = stage + 1 == NSTAGE ? 0 : stage + 1;
-    ++it;
+    if (!FAST) ++it;
     return false;
   };
   for (;;) {
@@ -554,7 +556,12 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     int f = (lrem < crem ? lrem : crem) - 1;
     if (n - LEAD - it < f) f = n - LEAD - it;
     if (c != c_prev) f = 0;
-    for (; f > 0; --f) pass(std::true_type{});
+    if (f > 0) {
+      for (int i = 0; i < f; ++i) pass(std::true_type{});
+      it += f;
+      lrem -= f;
+      crem -= f;
+    }
     if (pass(std::false_type{})) break;
   }
   if (grp_a) phase_barrier();   // matches group B's extra barrier at the start
