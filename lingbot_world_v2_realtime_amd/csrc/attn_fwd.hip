@@ -5,8 +5,9 @@
 // M axis, queries on N), so a lane holds one query and 16 keys of each 32x32 S tile: the row max and row sum
 // are in-lane plus one exchange with lane ^ 32 (v_permlane32_swap), and the S tile's register layout is directly
 // the B operand (P^T) of the PV product O^T = V^T P^T because the fp8 V block stores its keys in that order.
-// The int32 accumulator starts at the bits of 1.5 * 2^23, so its result reads directly as the float
-// 12582912 + S (|S| <= 2^21): the int -> float conversion is free. The two 4-wave halves of the workgroup run
+// The int32 accumulator starts at the bits of 1 / (2 pi) (an inline constant of the MFMA), so its result reads
+// directly as the float 1/(2 pi) + S * 2^-26 (|S| <= 2^21, one binade): the int -> float conversion is free, and
+// the logit scale carries the factor 2^26. The two 4-wave halves of the workgroup run
 // phase-shifted (one half's MFMAs under the other half's softmax); K / V blocks of 64 keys reach LDS by direct
 // global -> LDS loads several blocks ahead (see attend_range).
 //
@@ -181,6 +182,16 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
 
+// The first int8 MFMA of a QK^T accumulation, its accumulator operand the inline constant whose bits are S_MAGIC
+// (written as asm: the builtin folds only a zero accumulator into the instruction, any other constant tile is moved
+// into 16 registers first). The result then reads as the float S_MAGIC_F + s * 2^-26.
+__device__ __forceinline__ v16i mfma_i8_from_magic(v4i a, v4i b) {
+  static_assert(S_MAGIC == 0x3E22F983, "the asm below encodes this value");
+  v16i d;
+  asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0x3e22f983" : "=&v"(d) : "v"(a), "v"(b));
+  return d;
+}
+
 // A block's tiles (K, V and, with TWO, the V residual) in one asm, M0 saved once and restored once around the loads.
 // Each source is a wave-uniform base plus a 32-bit per-lane byte offset (the global instruction's scalar-base form:
 // no 64-bit address per lane to form).
@@ -235,15 +246,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) qf[kk] = *(const v4i*)(qrow + 16 * kk);
   }
-  const float qs_sl2 = q_scale[(int64_t)bh * (a.lp / QG) + (q0 >> 5)] * a.sl2;
+  // the logit scale per unit of the accumulator's float reading (2^-26 per integer step; exact power-of-2 factor)
+  const float qs_sl2 = q_scale[(int64_t)bh * (a.lp / QG) + (q0 >> 5)] * a.sl2 * S_MAGIC_INV_ULP;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) st.o[mt][i] = 0.f;
   float m_ref = -INFINITY, l_run = 0.f;
-  v16i magic;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) magic[i] = S_MAGIC;
   const bool multi = a.n_seg > 1;
 
   // fragment read offsets in a stage (K: chunk 4g + kk of row 32 mt + lq; V: chunks 2g, 2g + 1 of row 32 mt + lq)
@@ -413,8 +422,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     }
     __builtin_amdgcn_sched_barrier(0);
     if (do_qk) {
-      acc[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[0], qf[0], magic, 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[1], qf[0], magic, 0, 0, 0);
+      acc[0] = mfma_i8_from_magic(kf[0], qf[0]);
+      acc[1] = mfma_i8_from_magic(kf[1], qf[0]);
     }
     __builtin_amdgcn_sched_barrier(0);
     // DMA of block it + LEAD into the stage of block it - 2 (both groups finished it a phase ago): in the MFMA

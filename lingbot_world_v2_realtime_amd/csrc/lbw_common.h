@@ -25,8 +25,12 @@ constexpr float P_OFFSET = 8.807f;           // log2(448): P = exp2(s - m + P_OF
 // A row's reference max m moves only when a block's max exceeds it by more than RESCALE_SLACK (log2 units);
 // P = exp2(s - m + P_OFFSET - RESCALE_SLACK) then stays <= 448 and the O rescale is rare.
 constexpr float RESCALE_SLACK = 2.f;
-constexpr int S_MAGIC = 0x4B400000;          // int bits of 12582912.0f = 1.5 * 2^23
-constexpr float S_MAGIC_F = 12582912.f;      // float(S_MAGIC + s) == 12582912 + s for |s| < 2^22
+// The QK^T accumulator starts at the bits of S_MAGIC_F = 0x1.45f306p-3 (1 / (2 pi), an inline constant of the MFMA's
+// accumulator operand), whose binade [1/8, 1/4) has ulp 2^-26 and room for 2292099 steps down and 6096509 up: for an
+// int8 logit |s| <= 128 * 128 * 128 = 2^21, float(S_MAGIC + s) == S_MAGIC_F + s * 2^-26 exactly.
+constexpr int S_MAGIC = 0x3E22F983;
+constexpr float S_MAGIC_F = 0x1.45f306p-3f;
+constexpr float S_MAGIC_INV_ULP = 67108864.f;   // 2^26
 
 // Loads of data that is read once: the non-temporal hint streams it through the caches without keeping it
 // (measured on MI355X: 7.0-7.3 TB/s for a 1.1 GB read against 6.3-6.4 TB/s with plain loads).
