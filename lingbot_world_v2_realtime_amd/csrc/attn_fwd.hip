@@ -192,39 +192,41 @@ __device__ __forceinline__ v16i mfma_i8_from_magic(v4i a, v4i b) {
   return d;
 }
 
-// A block's tiles (K, V and, with TWO, the V residual) in one asm, M0 saved once and restored once around the loads.
-// Each source is a wave-uniform base plus a 32-bit per-lane byte offset (the global instruction's scalar-base form:
-// no 64-bit address per lane to form).
+// A block's loads in one asm, M0 saved once and restored once around them: the K, V and (with TWO) V-residual tiles,
+// 16 bytes per lane, then the block's 4-byte K scale by lane 0 alone (EXEC set to lane 0 around that load and
+// restored before the asm ends, so no branch). Each source is a wave-uniform base plus a 32-bit per-lane byte
+// offset (the global instruction's scalar-base form: no 64-bit address per lane to form).
 template <bool TWO>
-__device__ __forceinline__ void dma16_tiles(const void* kb, uint32_t koff, const void* vb, const void* vlb, uint32_t voff,
-                                            uint8_t* lk, uint8_t* lv, uint8_t* lvl) {
+__device__ __forceinline__ void dma_block(const void* kb, uint32_t koff, const void* vb, const void* vlb, uint32_t voff,
+                                          const void* ksb, uint8_t* lk, uint8_t* lv, uint8_t* lvl, uint8_t* lks) {
   uint32_t keep;
+  uint64_t ex;
+  const uint32_t zero = 0;
   if (TWO)
     asm volatile("s_mov_b32 %0, m0\n\t"
-                 "s_mov_b32 m0, %5\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
-                 "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %3, %4\n\t"
-                 "s_mov_b32 m0, %8\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %3, %7\n\t"
+                 "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\t"
+                 "s_mov_b32 m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %5\n\t"
+                 "s_mov_b32 m0, %9\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %8\n\t"
+                 "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 1\n\t"
+                 "s_mov_b32 m0, %12\n\ts_nop 0\n\tglobal_load_lds_dword %10, %11\n\t"
+                 "s_mov_b64 exec, %1\n\t"
                  "s_mov_b32 m0, %0"
-                 : "=&s"(keep)
+                 : "=&s"(keep), "=&s"(ex)
                  : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv)), "s"(vlb),
-                   "s"(lds_addr(lvl))
+                   "s"(lds_addr(lvl)), "v"(zero), "s"(ksb), "s"(lds_addr(lks))
                  : "memory");
   else
     asm volatile("s_mov_b32 %0, m0\n\t"
-                 "s_mov_b32 m0, %5\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
-                 "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %3, %4\n\t"
+                 "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\t"
+                 "s_mov_b32 m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %5\n\t"
+                 "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 1\n\t"
+                 "s_mov_b32 m0, %10\n\ts_nop 0\n\tglobal_load_lds_dword %8, %9\n\t"
+                 "s_mov_b64 exec, %1\n\t"
                  "s_mov_b32 m0, %0"
-                 : "=&s"(keep)
-                 : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv))
+                 : "=&s"(keep), "=&s"(ex)
+                 : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv)), "v"(zero), "s"(ksb),
+                   "s"(lds_addr(lks))
                  : "memory");
-}
-
-// 4 bytes per active lane (the block's K scale, issued by one lane)
-__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint8_t* lds) {
-  uint32_t keep;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\t"
-               "s_mov_b32 m0, %0"
-               : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
@@ -292,9 +294,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   seek(lc, lb);
   auto issue = [&](int stage) {
     uint8_t* sb = lds + stage * ST_BYTES + w * 1024;
-    dma16_tiles<TWO>(kbase, (uint32_t)koff, vbase, TWO ? (const void*)vlbase : nullptr, (uint32_t)voff, sb + ST_K,
-                     sb + ST_V, sb + ST_VLO);
-    if (lane == 0) dma4(ksbase, 0u, lds + TAB_KS + (stage * AT_WAVES + w) * 4);   // one lane: 4 bytes
+    dma_block<TWO>(kbase, (uint32_t)koff, vbase, TWO ? (const void*)vlbase : nullptr, (uint32_t)voff, ksbase,
+                   sb + ST_K, sb + ST_V, sb + ST_VLO, lds + TAB_KS + (stage * AT_WAVES + w) * 4);
   };
   auto advance = [&](auto fast) {   // fast: the next block is in the same chunk (lrem >= 2)
     if (!decltype(fast)::value && --lrem == 0) {   // the fast form's steps are taken off lrem after the run
@@ -360,6 +361,9 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     beta *= a.sl2;
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the table writes are done before the barrier below
   }
+  // per-row values that change only with m_ref or beta: the rescale threshold and the exponent's offset
+  float thr = m_ref + RESCALE_SLACK;
+  float tk = beta - m_ref + (P_OFFSET - RESCALE_SLACK);
   wait_vm(NPB * (npre - 1));   // every wave's piece of the first block has landed
   int ldstage = npre % NSTAGE;
   phase_barrier();
@@ -496,6 +500,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
           st.o[mt][4 * q + 3] *= r.w;
         }
       beta = bias_tab[c * QT];
+      tk = beta - m_ref + (P_OFFSET - RESCALE_SLACK);
       c_prev = c;
     }
     const float cb = qs_sl2 * ks;
@@ -514,7 +519,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     // reference max: moves only when this block's max exceeds it by more than RESCALE_SLACK
     const int mx = halves_max_i(max32i(si));
     const float m_blk = (__int_as_float(mx) - S_MAGIC_F) * cb + beta;
-    const bool moved = m_blk > m_ref + RESCALE_SLACK;
+    const bool moved = m_blk > thr;
     if (__builtin_expect(__any(moved), 0)) {   // wave-uniform and rare
       const float m_new = moved ? m_blk : m_ref;
       const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
@@ -524,8 +529,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
 #pragma unroll
         for (int i = 0; i < 16; ++i) st.o[mt][i] *= alpha;
       m_ref = m_new;
+      thr = m_ref + RESCALE_SLACK;
+      tk = beta - m_ref + (P_OFFSET - RESCALE_SLACK);
     }
-    const float kc = (beta - m_ref + (P_OFFSET - RESCALE_SLACK)) - S_MAGIC_F * cb;
+    const float kc = tk - S_MAGIC_F * cb;
     float p[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(si[i]), cb, kc));
