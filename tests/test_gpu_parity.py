@@ -315,6 +315,38 @@ def test_memory_ring_ragged_chunks():
     assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
 
 
+def test_memory_ring_many_short_chunks():
+    """Eight chunks (the most one call takes) of 64, 1, 128, 63, 200, 65, 130 and 64 keys: one-block and
+    one-key chunks, a chunk switch every one to four blocks, masked tails next to full blocks, so the block loop
+    keeps leaving and re-entering its steady state (and the loader crosses chunks every few blocks)."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    h, lq, cl = 2, 300, 200
+    lens = (64, 1, 128, 63, 200, 65, 130, 64)
+    g = torch.Generator().manual_seed(91)
+    ks, vs = [], []
+    for n in lens:
+        ks.append((torch.randn(1, n, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16())
+        vs.append(torch.randn(1, n, h, 128, generator=g).bfloat16())
+    q = torch.randn(1, lq, h, 128, generator=g).bfloat16()
+    ring = QuantKVRing(1, 1, h, cl, slots=len(lens), device=DEV)
+    for kk, vv in zip(ks[:-1], vs[:-1]):
+        ring.write(0, kk.to(DEV), vv.to(DEV))
+        ring.commit()
+    ring.write(0, ks[-1].to(DEV), vs[-1].to(DEV))
+    slots, seg = ring.attended()
+    assert [int(x) for x in seg] == list(lens), (slots, seg)
+    out = ring.attend(q.to(DEV), 0).float().cpu()
+    ref = emu.attention(q, [emu.requant(kk, vv) for kk, vv in zip(ks, vs)], schedule_gx=_gx())[None]
+    sd = emu.sdpa_fp32(q, torch.cat(ks, 1), torch.cat(vs, 1))[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    print(f"eight short chunks vs-emu mean {e_emu.mean():.3e}; vs-sdpa max {e_sd.max():.3e} mean {e_sd.mean():.3e}; "
+          f"emu vs-sdpa max {e_scheme.max():.3e} mean {e_scheme.mean():.3e}")
+    assert torch.isfinite(out).all()
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
+    assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
+
+
 def test_hnd_layout_same_bits():
     """tensor_layout="HND" ([B, H, L, 128]) reads the same elements through other strides: the output is the
     NHD call's, bit for bit, with a custom sm_scale, and it is close to fp32 SDPA."""
