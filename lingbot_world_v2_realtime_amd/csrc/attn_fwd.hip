@@ -379,7 +379,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   auto pass = [&](auto fast) -> bool {
     constexpr bool FAST = decltype(fast)::value;
     // ---- MFMA phase: S of block it, P V of block it - 1 ----
-    // (no wave priority raise here: with the fast pass form it cost 0.3 %, and raising the softmax phase's 0.2 %)
+    // (wave priorities stay equal: raising this phase's cost 0.3 % of kernel time, raising the softmax phase's 0.2 %)
     // LDS reads run ahead of the MFMAs that consume them: all eight K fragments and the first two V fragments
     // are requested before the first QK MFMA, and each later pair of V fragments before the MFMA pair ahead of
     // its consumers. The scheduling fences keep the compiler from sinking the reads next to their uses, which
