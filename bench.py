@@ -213,7 +213,7 @@ def profile_only(args, dev):
             ring.write(0, mk.to(dev), mv.to(dev))
             ring.commit()
         ring.write(0, k.to(dev), v.to(dev))
-        slots, lens = ring.attended()
+        slots, lens, _ = ring.attended()
         q = q.to(dev)
         q8, qs, bias = kernels.quant_q(q, "NHD", ring.cache, 0, slots)
         o = torch.empty_like(q)
@@ -295,7 +295,7 @@ def prologue_call(dev, ring, steps=50):
         (1 + 0.3 * torch.randn(H * D, device=dev, generator=g)).to(torch.bfloat16)
     rope = ChunkRope.for_chunk(rope_freqs(dev), (4, 29, 52), current_start=3 * CHUNK)
     k_out = torch.empty(1, CHUNK, H, D, device=dev, dtype=torch.bfloat16)
-    slots, _ = ring.attended()
+    slots, _, _ = ring.attended()
     stream = torch.cuda.current_stream(dev)
 
     def kpart():
@@ -481,7 +481,7 @@ def main():
     tops = ops / (ms_step * 1e-3) / 1e12
 
     # attention kernel alone, HIP events on the stream it is launched on
-    slots, lens = ring.attended()
+    slots, lens, _ = ring.attended()
     q8, qs, bias = kernels.quant_q(q, "NHD", ring.cache, 0, slots)
     o = torch.empty_like(q)
     stream = torch.cuda.current_stream(dev)

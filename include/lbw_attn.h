@@ -22,8 +22,9 @@
  *   k_scale fp32  [layers][slots][BH][nb]             amax / 127 of each 64-token block
  *   km      fp32  [layers][slots][BH][128]            per-(head, channel) chunk mean (a bf16 value)
  *   v8      uint8 [layers][slots][BH][nb][128][64]    e4m3 V, per 64-key block: [channel][position]
- *   v8lo    uint8 [layers][slots][BH][nb][128][64]    optional second e4m3 plane: (y - hi) * 16, y = V * 448 / amax
- *   v_scale fp32  [layers][slots][BH][128]            amax / 448 per (head, channel)
+ *   v8lo    uint8 [layers][slots][BH][nb][128][64]    optional second e4m3 plane: (y - hi) * 16, y = V / v_scale
+ *   v_scale fp32  [layers][slots][BH][128]            per (head, channel): the power of two 2^e with amax / 2^e
+ *                                                      in (224, 448] (amax floored at 1e-7), so y is exact
  * With the second plane, V = (hi + lo / 16) * v_scale to about 7 significant bits instead of 4.
  * Position p of a 64-key V block holds key 32*((p&31)>>4) + 8*((p>>2)&3) + 4*(p>>5) + (p&3).
  *
@@ -176,7 +177,10 @@ int lbw_quant_mx_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t rows_pa
 
 /*
  * Quantized attention of Q (from lbw_quant_q) over the chunks seg_slot[0..n_seg) of one layer's cache
- * (pointers already offset to that layer), chunk c holding seg_len[c] valid tokens (1..cap). Writes bf16
+ * (pointers already offset to that layer): chunk c is read over tokens [first, first + seg_len[c]) of its slot,
+ * first = seg_first[c] (seg_first null: every chunk from token 0), 1 <= seg_len[c] <= cap - first. The keys of a
+ * chunk's first and last 64-token blocks outside that range are masked, so a window may start and end anywhere
+ * in a chunk (the token window of lingbot/layers/kv_cache.py:23-81). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the
  * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA (a second fp8 product with the
  * residual plane, scaled by 2^-4, when v8lo is not null), fp32 accumulation, V scale
@@ -189,7 +193,7 @@ int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias,
                  int64_t batch, int64_t lq, int64_t heads,
                  const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
                  const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
-                 const int32_t* seg_len,
+                 const int32_t* seg_len, const int32_t* seg_first,
                  uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
                  float sm_scale, void* workspace, void* stream);
 
@@ -212,7 +216,7 @@ int lbw_attn_fwd_noalloc(const int8_t* q8, const float* q_scale, const float* bi
                          int64_t batch, int64_t lq, int64_t heads,
                          const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
                          const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
-                         const int32_t* seg_len,
+                         const int32_t* seg_len, const int32_t* seg_first,
                          uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
                          float sm_scale, void* stream);
 
@@ -226,13 +230,23 @@ int64_t lbw_attn_noalloc_scratch_bytes(void);
 int lbw_attn_workgroups_per_xcd(void);
 
 /*
- * Debug: int32 logits S[bh][i][j] = sum_d q8[bh][i][d] * k8[slot][bh][j][d] for i < Lp and j < cap, through
- * the same LDS tiles and int8 MFMA as lbw_attn_fwd. out is int32 [BH][Lp][cap]. Has no reference
- * counterpart; it exists to check the QK^T product bit for bit.
+ * Debug: lbw_attn_fwd (same arguments, same results in `out`) run by a checking build of the attention kernel
+ * that also writes, for every key block it processes, the raw words of its QK^T accumulator: the int8 MFMA's
+ * int32 sums started from S_MAGIC = 0x3E22F983 (the bits of 1 / (2 pi)), as the attention's softmax reads them,
+ * before any key mask. logits is int32 [BH][Lp][nb * 64] (Lp = lq rounded up to 256; nb = the sum over chunks of
+ * ceil((seg_first[c] % 64 + seg_len[c]) / 64), their blocks in call order): element [bh][i][64 j + t] is
+ * S_MAGIC + sum_d q8[bh][i][d] * k8[slot][bh][64 b + t][d] for key t of the slot block b that is block j. The
+ * same stages, direct-to-LDS loads, XOR swizzle, fragment reads and accumulator start as lbw_attn_fwd, so the
+ * int32 logits the attention uses can be checked bit for bit; read as a float, word w is exactly
+ * 1/(2 pi) + (w - S_MAGIC) * 2^-26. Has no reference counterpart.
  */
-int lbw_qk_logits_i32(const int8_t* q8, int64_t bh, int64_t lq,
-                      const int8_t* k8, int64_t slots, int64_t cap, int64_t slot,
-                      int32_t* out, void* stream);
+int lbw_qk_logits_i32(const int8_t* q8, const float* q_scale, const float* bias,
+                      int64_t batch, int64_t lq, int64_t heads,
+                      const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
+                      const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                      const int32_t* seg_len, const int32_t* seg_first,
+                      uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
+                      float sm_scale, int32_t* logits, void* workspace, void* stream);
 
 #ifdef __cplusplus
 }

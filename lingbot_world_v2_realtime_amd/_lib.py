@@ -25,14 +25,15 @@ SIGNATURES = {
                                   _f32, _p]),
     "lbw_quant_rows_fp8": (_i32, [_p, _i32, _i64, _i64, _i64, _p, _p, _p]),
     "lbw_quant_mx_fp8": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p]),
-    "lbw_attn_fwd": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p,
+    "lbw_attn_fwd": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p,
                             _p, _i64, _i64, _i64, _f32, _p, _p]),
     "lbw_attn_workspace_bytes": (_i64, []),
-    "lbw_attn_fwd_noalloc": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p,
+    "lbw_attn_fwd_noalloc": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p,
                                     _p, _i64, _i64, _i64, _f32, _p]),
     "lbw_attn_noalloc_scratch_bytes": (_i64, []),
     "lbw_attn_workgroups_per_xcd": (_i32, []),
-    "lbw_qk_logits_i32": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _p, _p]),
+    "lbw_qk_logits_i32": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p,
+                                 _p, _i64, _i64, _i64, _f32, _p, _p, _p]),
 }
 
 

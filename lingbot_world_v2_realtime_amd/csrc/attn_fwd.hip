@@ -34,7 +34,9 @@ struct AttnArgs {
   float sl2;                       // sm_scale * log2(e)
   int n_seg, nb, q_tiles, n_tiles, gx;
   int seg_slot[LBW_MAX_SEGMENTS];
-  int seg_len[LBW_MAX_SEGMENTS];
+  int seg_fb[LBW_MAX_SEGMENTS];         // the slot block holding the chunk's first attended key
+  int seg_lead[LBW_MAX_SEGMENTS];       // keys of that block before the first attended one (masked)
+  int seg_span[LBW_MAX_SEGMENTS];       // keys from the start of block seg_fb to the last attended key
   int seg_blk0[LBW_MAX_SEGMENTS + 1];   // first tile-relative block of each chunk; [n_seg] = nb
   int split0[XCDS_MAX + 1];             // split tiles of XCDs before x (prefix), for the merge grid
 };
@@ -55,31 +57,9 @@ __device__ __forceinline__ XcdPlan xcd_plan(const AttnArgs& a, int x) {
   return p;
 }
 
-// K tile of the debug logits kernel in LDS: 64 rows x 128 bytes with rows padded to 144 bytes. The row stride
-// of 9 sixteen-byte units is odd, so the 16 lanes an LDS b128 access serves at a time (16 consecutive rows,
-// same chunk) hit 16 distinct bank groups. (The attention's stages XOR-swizzle their chunks instead.)
-constexpr int K_ROW = 144;
-constexpr int K_LDS = KB * K_ROW;              // 9216
 constexpr int S_MASKED = (int)0xFF800000;      // bits of -inf: the int max ignores it, exp2 gives 0
-__device__ __forceinline__ int k_lds_off(int row, int ch) { return row * K_ROW + (ch << 4); }
 constexpr int E8M0_ONE = 0x7F7F7F7F;           // MFMA block scale 1.0 in every byte
 constexpr int E8M0_LO = 0x7B7B7B7B;            // 2^-4: the lo plane carries (y - hi) * 16
-
-// S^T tile pair for 64 keys x 32 queries of this wave: acc[mt] covers keys 32 mt .. 32 mt + 31. `init` is the
-// accumulator start value, a loop-invariant register tile (no per-block moves).
-__device__ __forceinline__ void qk_tile(const uint8_t* sk, const v4i* qf, int lq, int g, v16i* acc, const v16i& init) {
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int row = 32 * mt + lq;
-    v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(*(const v4i*)(sk + k_lds_off(row, 4 * g)), qf[0], init, 0, 0, 0);
-#pragma unroll
-    for (int kk = 1; kk < 4; ++kk) {
-      const v4i kf = *(const v4i*)(sk + k_lds_off(row, 4 * g + kk));
-      c = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[kk], c, 0, 0, 0);
-    }
-    acc[mt] = c;
-  }
-}
 
 // max / sum of a value over the two lane halves (lanes l and l ^ 32 hold the same query)
 __device__ __forceinline__ int halves_max_i(int x) {
@@ -231,13 +211,15 @@ __device__ __forceinline__ void dma_block(const void* kb, uint32_t koff, const v
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
-template <bool TWO>
+// LOGITS (a checking build): each block's raw QK^T accumulator words, S_MAGIC + S, also go to
+// logits[bh][q0 + row][64 j + key] (int32 [BH][Lp][nb * 64]) right after the QK MFMAs, before any mask.
+template <bool TWO, bool LOGITS>
 __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __restrict__ q8,
                                              const float* __restrict__ q_scale, const float* __restrict__ bias,
                                              const int8_t* __restrict__ k8, const float* __restrict__ k_scale,
                                              const uint8_t* __restrict__ v8, const uint8_t* __restrict__ v8lo,
                                              const float* __restrict__ v_scale, uint8_t* lds, int bh, int64_t q0,
-                                             int j0, int j1, Piece& st) {
+                                             int j0, int j1, Piece& st, int32_t* __restrict__ logits) {
   constexpr int NPB = TWO ? 4 : 3;   // DMA instructions per block of each wave (tiles + the K scale)
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform, so the loader's control stays scalar
@@ -285,12 +267,13 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   const uint8_t* vbase;
   const uint8_t* vlbase;
   const float* ksbase;
-  auto seek = [&](int cc, int bb) {
+  auto seek = [&](int cc, int bb) {   // block bb of chunk cc's range, i.e. slot block seg_fb[cc] + bb
     const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
-    kbase = k8 + (sbh * a.cap + (int64_t)bb * KB) * D;
-    vbase = v8 + (sbh * a.nbc + bb) * TILE_BYTES;
-    if (TWO) vlbase = v8lo + (sbh * a.nbc + bb) * TILE_BYTES;
-    ksbase = k_scale + sbh * a.nbc + bb;
+    const int64_t blk = (int64_t)bb + a.seg_fb[cc];
+    kbase = k8 + (sbh * a.cap + blk * KB) * D;
+    vbase = v8 + (sbh * a.nbc + blk) * TILE_BYTES;
+    if (TWO) vlbase = v8lo + (sbh * a.nbc + blk) * TILE_BYTES;
+    ksbase = k_scale + sbh * a.nbc + blk;
   };
   seek(lc, lb);
   auto issue = [&](int stage) {
@@ -317,8 +300,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int c = 0;
   while (j0 >= a.seg_blk0[c + 1]) ++c;
   int crem = a.seg_blk0[c + 1] - j0;                   // blocks left in chunk c, this one included
-  int last_valid = a.seg_len[c] - (a.seg_blk0[c + 1] - a.seg_blk0[c] - 1) * KB;   // keys in its last block
+  int last_valid = a.seg_span[c] - (a.seg_blk0[c + 1] - a.seg_blk0[c] - 1) * KB;   // keys in its last block
+  int lead = j0 == a.seg_blk0[c] ? a.seg_lead[c] : 0;  // leading keys of this block outside chunk c's range
   int c_prev = c;
+  int jd = j0;                                         // LOGITS: tile-relative block of the softmax phase
 
   // chunk tables: their global loads go out before the first blocks' DMA, so waiting for them waits for
   // nothing else. The previous piece's readers are done: it ended with a workgroup barrier.
@@ -509,13 +494,25 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) si[16 * mt + i] = acc[mt][i];
-    const int valid = FAST || crem != 1 ? KB : last_valid;   // keys of this block that exist (>= 1)
-    if (!FAST && valid < KB) {
-      const int vt = valid - 4 * g;   // key 32 mt + 8 (i >> 2) + 4 g + (i & 3) is past the end iff its
-#pragma unroll                        // lane-independent part reaches vt
-      for (int i = 0; i < 32; ++i)
-        if (32 * (i >> 4) + 8 * ((i >> 2) & 3) + (i & 3) >= vt) si[i] = S_MASKED;
+    if constexpr (LOGITS) {   // the raw accumulator words of block jd, then nothing left in flight but the DMA
+      int32_t* lrow = logits + ((int64_t)bh * a.lp + q0 + lq) * ((int64_t)a.nb * KB) + (int64_t)jd * KB + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) lrow[32 * (i >> 4) + 8 * ((i >> 2) & 3) + (i & 3)] = si[i];
+      wait_vm(0);
+      ++jd;
     }
+    const int valid = FAST || crem != 1 ? KB : last_valid;   // keys of this block that exist (>= 1)
+    if (!FAST && (valid < KB || lead > 0)) {
+      // key 32 mt + 8 (i >> 2) + 4 g + (i & 3) is past the end iff its lane-independent part reaches vt, and
+      // before the chunk's first attended key iff that part is below lt
+      const int vt = valid - 4 * g, lt = lead - 4 * g;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int kk = 32 * (i >> 4) + 8 * ((i >> 2) & 3) + (i & 3);
+        if (kk >= vt || kk < lt) si[i] = S_MASKED;
+      }
+    }
+    if (!FAST) lead = 0;
     // reference max: moves only when this block's max exceeds it by more than RESCALE_SLACK
     const int mx = halves_max_i(max32i(si));
     const float m_blk = (__int_as_float(mx) - S_MAGIC_F) * cb + beta;
@@ -549,7 +546,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     if (!FAST && --crem == 0 && c + 1 < a.n_seg) {   // the fast form's steps are taken off crem after the run
       ++c;
       crem = a.seg_blk0[c + 1] - a.seg_blk0[c];
-      last_valid = a.seg_len[c] - (crem - 1) * KB;
+      last_valid = a.seg_span[c] - (crem - 1) * KB;
+      lead = a.seg_lead[c];
     }
     if (FAST || grp_a) {   // A's pieces of block it + 1 have landed (blocks up to it + LEAD may still be in flight)
       if (FAST || it + LEAD < n) {   // steady state as one constant wait (a general count is a chain of branches)
@@ -567,11 +565,11 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   };
   for (;;) {
     // passes from here on that take the fast form: the loader stays in its chunk for f more blocks, block it is
-    // not its chunk's first (c == c_prev) and none of the f blocks is its chunk's last, and block it + f - 1 + LEAD
-    // still exists
+    // not its chunk's first (c == c_prev) nor a block with masked leading keys, none of the f blocks is its
+    // chunk's last, and block it + f - 1 + LEAD still exists
     int f = (lrem < crem ? lrem : crem) - 1;
     if (n - LEAD - it < f) f = n - LEAD - it;
-    if (c != c_prev) f = 0;
+    if (c != c_prev || lead > 0) f = 0;
     if (f > 0) {
       for (int i = 0; i < f; ++i) pass(std::true_type{});
       it += f;
@@ -633,7 +631,7 @@ __device__ __forceinline__ void store_part(const AttnArgs& a, const Piece& st, c
   if (g == 0) *(float2*)(ml_part + (slot_idx * QT + row) * 2) = make_float2(st.m, st.l);
 }
 
-template <bool TWO>
+template <bool TWO, bool LOGITS>
 __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* __restrict__ q8,
                                                                  const float* __restrict__ q_scale,
                                                                  const float* __restrict__ bias,
@@ -643,7 +641,8 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* _
                                                                  const uint8_t* __restrict__ v8lo,
                                                                  const float* __restrict__ v_scale,
                                                                  uint16_t* __restrict__ out, float* __restrict__ o_part,
-                                                                 float* __restrict__ ml_part, AttnArgs a) {
+                                                                 float* __restrict__ ml_part, int32_t* __restrict__ logits,
+                                                                 AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[AT_LDS];
   const int gid = blockIdx.x, x = gid % XCDS, i = gid / XCDS;
   const int w = threadIdx.x >> 6;
@@ -653,7 +652,7 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* _
   for (int tile = p.t_lo + i; tile < p.ts; tile += a.gx) {
     const int bh = tile / a.q_tiles;
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
-    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, 0, a.nb, st);
+    attend_range<TWO, LOGITS>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, 0, a.nb, st, logits);
     store_out(a, st, v_scale, out, bh, q0);
   }
   // this workgroup's piece of the split tiles
@@ -666,7 +665,7 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* _
     const int j1 = (int)((u1 - u + j0 < a.nb) ? (u1 - u + j0) : a.nb);
     const int bh = tile / a.q_tiles;
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
-    attend_range<TWO>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, j0, j1, st);
+    attend_range<TWO, LOGITS>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, j0, j1, st, logits);
     if (j0 == 0 && j1 == a.nb) {
       store_out(a, st, v_scale, out, bh, q0);
     } else {
@@ -760,36 +759,6 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   *(uint2*)(dst + 4) = make_uint2(w[2], w[3]);
 }
 
-// Debug: S = q8 . k8^T in int32 for one slot, on the same int8 MFMA as the attention (128 queries per workgroup).
-constexpr int LOGIT_ROWS = 128;
-__global__ __launch_bounds__(256) void qk_logits_kernel(const int8_t* __restrict__ q8,
-                                                        const int8_t* __restrict__ k8, int64_t lp,
-                                                        int64_t cap, int64_t bh_count, int64_t slot,
-                                                        int32_t* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[K_LDS];
-  const int tile = blockIdx.x, blk = blockIdx.y, bh = blockIdx.z;
-  const int t = threadIdx.x, w = t >> 6, lane = t & 63, lq = lane & 31, g = lane >> 5;
-  const int64_t q0 = (int64_t)tile * LOGIT_ROWS + w * 32;
-  v4i qf[4];
-  const int8_t* qrow = q8 + ((int64_t)bh * lp + q0 + lq) * D + 64 * g;
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) qf[kk] = *(const v4i*)(qrow + 16 * kk);
-  const int8_t* kp = k8 + ((slot * bh_count + bh) * cap + (int64_t)blk * KB) * D;
-  *(v4i*)(smem + k_lds_off(t >> 3, t & 7)) = *(const v4i*)(kp + t * 16);
-  *(v4i*)(smem + k_lds_off((t >> 3) + 32, t & 7)) = *(const v4i*)(kp + 4096 + t * 16);
-  __syncthreads();
-  v16i zero;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) zero[i] = 0;
-  v16i acc[2];
-  qk_tile(smem, qf, lq, g, acc, zero);
-  int32_t* op = out + ((int64_t)bh * lp + q0 + lq) * cap + (int64_t)blk * KB;
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) op[32 * mt + 8 * (i >> 2) + 4 * g + (i & 3)] = acc[mt][i];
-}
-
 // Persistent workgroups per XCD: one per CU (a workgroup is 8 waves, two per SIMD, and uses AT_LDS bytes of the
 // CU's 160 KB of LDS). Cached per device ordinal; atomic, since entry points may run on several host threads.
 static int attn_wgs_per_xcd() {
@@ -817,12 +786,14 @@ extern "C" int64_t lbw_attn_workspace_bytes(void) {
   return (int64_t)XCDS * gx * 2 * QT * (D + 2) * (int64_t)sizeof(float);
 }
 
-extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
-                            int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
-                            const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
-                            int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len, uint16_t* out,
-                            int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head, float sm_scale,
-                            void* workspace, void* stream) {
+// The checks and launches of lbw_attn_fwd; with `logits` not null the checking build of the kernel also writes
+// every block's raw QK^T accumulator words there.
+static int attn_launch(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch, int64_t lq,
+                       int64_t heads, const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
+                       const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                       const int32_t* seg_len, const int32_t* seg_first, uint16_t* out, int64_t o_s_batch,
+                       int64_t o_s_tok, int64_t o_s_head, float sm_scale, int32_t* logits, void* workspace,
+                       void* stream) {
   if (!q8 || !q_scale || !k8 || !k_scale || !v8 || !v_scale || !out || !seg_slot || !seg_len || !workspace)
     return LBW_E_NULL;
   if (batch <= 0 || heads <= 0 || lq <= 0 || slots <= 0 || cap <= 0 || cap % KB) return LBW_E_SHAPE;
@@ -831,7 +802,7 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   if (n_seg > 1 && !bias) return LBW_E_NULL;
   if (o_s_batch % 4 || o_s_tok % 4 || o_s_head % 4) return LBW_E_ALIGN;
   if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo | (uintptr_t)workspace) & 15 ||
-      ((uintptr_t)out & 7))
+      ((uintptr_t)out & 7) || ((uintptr_t)logits & 3))
     return LBW_E_ALIGN;
   AttnArgs a;
   a.lq = lq;
@@ -845,13 +816,17 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   a.n_seg = n_seg;
   int nb = 0;
   for (int c = 0; c <= LBW_MAX_SEGMENTS; ++c) a.seg_blk0[c] = 0;
-  for (int c = 0; c < LBW_MAX_SEGMENTS; ++c) { a.seg_slot[c] = 0; a.seg_len[c] = 0; }
+  for (int c = 0; c < LBW_MAX_SEGMENTS; ++c) a.seg_slot[c] = a.seg_fb[c] = a.seg_lead[c] = a.seg_span[c] = 0;
   for (int c = 0; c < n_seg; ++c) {
-    if (seg_slot[c] < 0 || seg_slot[c] >= slots || seg_len[c] < 1 || seg_len[c] > cap) return LBW_E_SEGMENTS;
+    const int first = seg_first ? seg_first[c] : 0;
+    if (seg_slot[c] < 0 || seg_slot[c] >= slots || seg_len[c] < 1 || first < 0 || seg_len[c] > cap - first)
+      return LBW_E_SEGMENTS;
     a.seg_slot[c] = seg_slot[c];
-    a.seg_len[c] = seg_len[c];
+    a.seg_fb[c] = first / KB;
+    a.seg_lead[c] = first % KB;
+    a.seg_span[c] = first % KB + seg_len[c];
     a.seg_blk0[c] = nb;
-    nb += (seg_len[c] + KB - 1) / KB;
+    nb += (a.seg_span[c] + KB - 1) / KB;
   }
   for (int c = n_seg; c <= LBW_MAX_SEGMENTS; ++c) a.seg_blk0[c] = nb;
   a.nb = nb;
@@ -868,17 +843,45 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
   float* o_part = (float*)workspace;
   float* ml_part = o_part + (int64_t)XCDS * a.gx * 2 * QT * D;
   hipStream_t st = (hipStream_t)stream;
-  if (v8lo)
-    hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3((unsigned)(XCDS * a.gx)), dim3(AT_THREADS), 0, st, q8, q_scale, bias,
-                       k8, k_scale, v8, v8lo, v_scale, out, o_part, ml_part, a);
+  const dim3 grid((unsigned)(XCDS * a.gx)), block(AT_THREADS);
+  if (v8lo && logits)
+    hipLaunchKernelGGL((attn_fwd_kernel<true, true>), grid, block, 0, st, q8, q_scale, bias, k8, k_scale, v8, v8lo,
+                       v_scale, out, o_part, ml_part, logits, a);
+  else if (v8lo)
+    hipLaunchKernelGGL((attn_fwd_kernel<true, false>), grid, block, 0, st, q8, q_scale, bias, k8, k_scale, v8, v8lo,
+                       v_scale, out, o_part, ml_part, logits, a);
+  else if (logits)
+    hipLaunchKernelGGL((attn_fwd_kernel<false, true>), grid, block, 0, st, q8, q_scale, bias, k8, k_scale, v8, v8lo,
+                       v_scale, out, o_part, ml_part, logits, a);
   else
-    hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3((unsigned)(XCDS * a.gx)), dim3(AT_THREADS), 0, st, q8, q_scale, bias,
-                       k8, k_scale, v8, v8lo, v_scale, out, o_part, ml_part, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, block, 0, st, q8, q_scale, bias, k8, k_scale, v8, v8lo,
+                       v_scale, out, o_part, ml_part, logits, a);
   if (a.split0[XCDS] > 0)
     hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(a.split0[XCDS] * (QT / MERGE_ROWS))), dim3(256), 0, st,
                        o_part, ml_part, out, a);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
+}
+
+extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
+                            int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
+                            const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
+                            int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
+                            const int32_t* seg_first, uint16_t* out, int64_t o_s_batch, int64_t o_s_tok,
+                            int64_t o_s_head, float sm_scale, void* workspace, void* stream) {
+  return attn_launch(q8, q_scale, bias, batch, lq, heads, k8, k_scale, v8, v8lo, v_scale, slots, cap, n_seg, seg_slot,
+                     seg_len, seg_first, out, o_s_batch, o_s_tok, o_s_head, sm_scale, nullptr, workspace, stream);
+}
+
+extern "C" int lbw_qk_logits_i32(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
+                                 int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
+                                 const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
+                                 int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
+                                 const int32_t* seg_first, uint16_t* out, int64_t o_s_batch, int64_t o_s_tok,
+                                 int64_t o_s_head, float sm_scale, int32_t* logits, void* workspace, void* stream) {
+  if (!logits) return LBW_E_NULL;
+  return attn_launch(q8, q_scale, bias, batch, lq, heads, k8, k_scale, v8, v8lo, v_scale, slots, cap, n_seg, seg_slot,
+                     seg_len, seg_first, out, o_s_batch, o_s_tok, o_s_head, sm_scale, logits, workspace, stream);
 }
 
 // ---- the entry point that allocates nothing -----------------------------------------------------------------
@@ -910,25 +913,12 @@ extern "C" int lbw_attn_fwd_noalloc(const int8_t* q8, const float* q_scale, cons
                                     int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
                                     const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
                                     int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
-                                    uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
-                                    float sm_scale, void* stream) {
+                                    const int32_t* seg_first, uint16_t* out, int64_t o_s_batch, int64_t o_s_tok,
+                                    int64_t o_s_head, float sm_scale, void* stream) {
   if (const int dv = check_device()) return dv;
   if (lbw_attn_workspace_bytes() > ATTN_SCRATCH_BYTES) return LBW_E_SCRATCH;   // more CUs than the array covers
   void* ws = scratch_on_current_device();
   if (!ws) return LBW_E_DEVICE;
-  return lbw_attn_fwd(q8, q_scale, bias, batch, lq, heads, k8, k_scale, v8, v8lo, v_scale, slots, cap, n_seg,
-                      seg_slot, seg_len, out, o_s_batch, o_s_tok, o_s_head, sm_scale, ws, stream);
-}
-
-extern "C" int lbw_qk_logits_i32(const int8_t* q8, int64_t bh, int64_t lq, const int8_t* k8, int64_t slots,
-                                 int64_t cap, int64_t slot, int32_t* out, void* stream) {
-  if (!q8 || !k8 || !out) return LBW_E_NULL;
-  if (bh <= 0 || bh > 65535 || lq <= 0 || cap <= 0 || cap % KB || slot < 0 || slot >= slots) return LBW_E_SHAPE;
-  if (((uintptr_t)q8 | (uintptr_t)k8) & 15) return LBW_E_ALIGN;
-  if (const int dv = check_device()) return dv;
-  const int64_t lp = (lq + QT - 1) / QT * QT;
-  hipLaunchKernelGGL(qk_logits_kernel, dim3((unsigned)(lp / LOGIT_ROWS), (unsigned)(cap / KB), (unsigned)bh), dim3(256),
-                     0, (hipStream_t)stream, q8, k8, lp, cap, bh, slot, out);
-  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
-  return LBW_OK;
+  return attn_launch(q8, q_scale, bias, batch, lq, heads, k8, k_scale, v8, v8lo, v_scale, slots, cap, n_seg, seg_slot,
+                     seg_len, seg_first, out, o_s_batch, o_s_tok, o_s_head, sm_scale, nullptr, ws, stream);
 }

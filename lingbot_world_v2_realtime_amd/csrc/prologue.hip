@@ -99,9 +99,12 @@ __device__ __forceinline__ void load_rows(uint32_t (&x)[2][4][4], const uint16_t
     }
 }
 
-// x (from load_rows) normalised, weighted and roped in place.
+// x (from load_rows; rows row0 .. row0 + 31) normalised, weighted and roped in place. Rows past the chunk get
+// the scale 0, so they stay exact zeros for any eps (with eps = 0, 1 / sqrt(0 + eps) would make them NaN and
+// spoil the group's Q scale and the half block's column sums).
 __device__ __forceinline__ void norm_rope_rows(uint32_t (&x)[2][4][4], const uint16_t* __restrict__ w,
-                                               const ProArgs& a, double* s_ss, float* s_r, const double2* s_cs) {
+                                               const ProArgs& a, int64_t row0, double* s_ss, float* s_r,
+                                               const double2* s_cs) {
   const int lane = threadIdx.x & 63, h = threadIdx.x >> 6, rq = lane >> 4, g = lane & 15;
   double ss[2][4];
 #pragma unroll
@@ -131,7 +134,7 @@ __device__ __forceinline__ void norm_rope_rows(uint32_t (&x)[2][4][4], const uin
     double tot = 0.0;
     for (int hh = 0; hh < a.heads; ++hh) tot = tot + s_ss[threadIdx.x * PRO_MAX_HEADS + hh];
     const float ms = (float)(tot / (double)(a.heads * D));
-    s_r[threadIdx.x] = (float)(1.0 / sqrt((double)(ms + a.eps)));
+    s_r[threadIdx.x] = row0 + threadIdx.x < a.len ? (float)(1.0 / sqrt((double)(ms + a.eps))) : 0.f;
   }
   __syncthreads();
   const v4i wv = *(const v4i*)(w + h * D + g * 8);
@@ -179,7 +182,7 @@ __global__ __launch_bounds__(MAXT) void norm_rope_q_kernel(const uint16_t* __res
   load_rows(x, q + b * a.x_sb, a, row0);
   stage_rope(s_cs, tab, a, row0);
   if (a.n_seg > 1) stage_means(s_km, km, a, b);   // norm_rope_rows' barriers order the staging before the reads
-  norm_rope_rows(x, w, a, s_ss, s_r, s_cs);
+  norm_rope_rows(x, w, a, row0, s_ss, s_r, s_cs);
   float amax = 0.f;
 #pragma unroll
   for (int s = 0; s < 2; ++s)
@@ -279,7 +282,7 @@ __global__ __launch_bounds__(MAXT) void norm_rope_k_kernel(const uint16_t* __res
 #pragma unroll
       for (int e = 0; e < 8; ++e) part_amax[o + e] = vmax[e];
   }
-  norm_rope_rows(x, w, a, s_ss, s_r, s_cs);
+  norm_rope_rows(x, w, a, row0, s_ss, s_r, s_cs);
   uint16_t* ko = k_out + b * a.o_sb + h * a.o_sh + g * 8;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {

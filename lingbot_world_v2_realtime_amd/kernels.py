@@ -331,15 +331,29 @@ def attn_workspace(device, stream=None):
     return _ATTN_WS[key]
 
 
+def key_blocks(seg_lens, seg_firsts=None):
+    """64-key blocks the attention walks over chunks read over [first, first + len) of their slots."""
+    firsts = seg_firsts or [0] * len(seg_lens)
+    return sum((f % K_BLOCK + n + K_BLOCK - 1) // K_BLOCK for f, n in zip(firsts, seg_lens))
+
+
 def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_lens, out, layout="NHD",
-             sm_scale=None, workspace=None, noalloc=False):
-    """Quantized attention of quantised Q over the chunks `seg_slots` (with `seg_lens` valid tokens) of one
-    layer of `ring`, written into bf16 `out` ([B, Lq, H, 128] NHD or [B, H, Lq, 128] HND). noalloc=True calls
-    lbw_attn_fwd_noalloc, whose scratch is the library's fixed per-GPU array (no workspace)."""
+             sm_scale=None, workspace=None, noalloc=False, seg_firsts=None, logits=None):
+    """Quantized attention of quantised Q over the chunks `seg_slots` of one layer of `ring`, chunk c read over
+    tokens [seg_firsts[c], seg_firsts[c] + seg_lens[c]) of its slot (seg_firsts None: from token 0), written into
+    bf16 `out` ([B, Lq, H, 128] NHD or [B, H, Lq, 128] HND). noalloc=True calls lbw_attn_fwd_noalloc, whose scratch
+    is the library's fixed per-GPU array (no workspace). logits: an int32 [BH, Lp, 64 * key_blocks] tensor makes
+    the call run the kernel's checking build (lbw_qk_logits_i32), which also writes each block's raw QK^T
+    accumulator words there."""
     lib = _lib.load()
     n_seg = len(seg_slots)
     if not 1 <= n_seg <= MAX_SEGMENTS or len(seg_lens) != n_seg:
         raise ValueError(f"need 1..{MAX_SEGMENTS} chunks with a length each, got {seg_slots} / {seg_lens}")
+    if seg_firsts is not None and len(seg_firsts) != n_seg:
+        raise ValueError(f"need a first token per chunk, got {seg_firsts} for {n_seg} chunks")
+    if any(int(n) < 1 for n in seg_lens) or any(int(f) < 0 or int(f) + int(n) > ring.cap for f, n in
+                                                zip(seg_firsts or [0] * n_seg, seg_lens)):
+        raise ValueError(f"chunk ranges (first {seg_firsts}, length {seg_lens}) must lie in slots of {ring.cap}")
     _require_cuda_bf16("out", out)
     _same_device("attn_fwd", q8, q_scale, bias, out, ring.k8, workspace)
     ob, ol, oh, o_b, o_t, o_h = _dims(out, layout)
@@ -365,30 +379,50 @@ def attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_le
     k8, ksc, _, v8, v8lo, vsc = ring.layer_view(layer)
     slot_arr = (ctypes_i32 * n_seg)(*seg_slots)
     len_arr = (ctypes_i32 * n_seg)(*seg_lens)
+    first_arr = (ctypes_i32 * n_seg)(*seg_firsts) if seg_firsts is not None else None
     if noalloc:
+        if logits is not None:
+            raise ValueError("the checking build runs through lbw_qk_logits_i32, which takes a workspace")
         st = lib.lbw_attn_fwd_noalloc(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
                                       _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr,
-                                      _ptr(out), o_b, o_t, o_h, sm_scale, _stream(q8))
+                                      first_arr, _ptr(out), o_b, o_t, o_h, sm_scale, _stream(q8))
         _lib.check(st, "lbw_attn_fwd_noalloc")
         return out
     if workspace is None:
         workspace = attn_workspace(q8.device, _stream(q8))
+    if logits is not None:
+        want = (bh, lp, K_BLOCK * key_blocks(seg_lens, seg_firsts))
+        if logits.dtype != torch.int32 or tuple(logits.shape) != want or not logits.is_contiguous():
+            raise ValueError(f"logits must be contiguous int32 {want}, got {logits.dtype} {tuple(logits.shape)}")
+        _same_device("qk_logits", q8, logits)
+        st = lib.lbw_qk_logits_i32(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
+                                   _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr,
+                                   first_arr, _ptr(out), o_b, o_t, o_h, sm_scale, _ptr(logits), _ptr(workspace),
+                                   _stream(q8))
+        _lib.check(st, "lbw_qk_logits_i32")
+        return out
     st = lib.lbw_attn_fwd(_ptr(q8), _ptr(q_scale), _ptr(bias), batch, lq, heads, _ptr(k8), _ptr(ksc),
-                          _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr, _ptr(out),
-                          o_b, o_t, o_h, sm_scale, _ptr(workspace), _stream(q8))
+                          _ptr(v8), _ptr(v8lo), _ptr(vsc), ring.slots, ring.cap, n_seg, slot_arr, len_arr, first_arr,
+                          _ptr(out), o_b, o_t, o_h, sm_scale, _ptr(workspace), _stream(q8))
     _lib.check(st, "lbw_attn_fwd")
     return out
 
 
-def qk_logits(q8, lq, ring, layer, slot):
-    """Debug: int32 S [BH, Lp, cap] of quantised Q against one slot, via the attention's MFMA tiles."""
-    lib = _lib.load()
-    bh, lp = q8.shape[0], q8.shape[1]
-    out = torch.empty(bh, lp, ring.cap, dtype=torch.int32, device=q8.device)
-    st = lib.lbw_qk_logits_i32(_ptr(q8), bh, lq, _ptr(ring.k8[layer]), ring.slots, ring.cap, slot, _ptr(out),
-                               _stream(q8))
-    _lib.check(st, "lbw_qk_logits_i32")
-    return out
+# S_MAGIC: the bits of 1 / (2 pi), where the attention kernel's int32 QK^T accumulators start
+S_MAGIC = 0x3E22F983
+
+
+def qk_logits(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_lens, seg_firsts=None,
+              sm_scale=None):
+    """Debug: the attention call of attn_fwd run by the kernel's checking build, returning (raw, out): raw is
+    int32 [BH, Lp, 64 * key_blocks] holding every key block's QK^T accumulator words S_MAGIC + q8 . k8 (blocks
+    in call order, each the 64 keys of a slot block), out the attention output [B, Lq, H, 128] bf16."""
+    bh, lp = batch * heads, pad_to(lq, Q_TILE)
+    raw = torch.empty(bh, lp, K_BLOCK * key_blocks(seg_lens, seg_firsts), dtype=torch.int32, device=q8.device)
+    out = torch.empty(batch, lq, heads, HEAD_DIM, dtype=torch.bfloat16, device=q8.device)
+    attn_fwd(q8, q_scale, bias, batch, lq, heads, ring, layer, seg_slots, seg_lens, out, "NHD", sm_scale,
+             seg_firsts=seg_firsts, logits=raw)
+    return raw, out
 
 
 def _dims(x, layout):

@@ -14,10 +14,12 @@ forward can be captured in a HIP graph. Two ways to choose what a forward attend
   `sink_chunks` saved chunks kept for good (a slot-granular version of model_fast_kv_ring.py:28-48's ring).
 - The reference's token window (`sink_tokens` / `window_tokens`, or `from_frames`): exactly the tokens
   lingbot/layers/kv_cache.py:23-81 keeps -- a sink of the rollout's first `sink_tokens` tokens plus the most
-  recent ones, `window_tokens` in all, evicting by shift. Here nothing moves: a chunk stays in its slot and the
-  attention reads the prefix of it that the sink still covers (a per-chunk key count), so the reference's
-  default `--sink_size 6 --local_attn_size 18` with 4-frame chunks of 1508-token frames attends chunk 0, the
-  first 3016 tokens of chunk 1, the two latest saved chunks and the current chunk: 27144 keys in 5 slots.
+  recent ones, `window_tokens` in all, evicting by shift, the last `max_attention_size` of them attended.
+  Here nothing moves: a chunk stays in its slot and the attention reads the range of it that the window still
+  covers (a first token and a key count per chunk, any token of the chunk), so the reference's default
+  `--sink_size 6 --local_attn_size 18` with 4-frame chunks of 1508-token frames attends chunk 0, the first 3016
+  tokens of chunk 1, the two latest saved chunks and the current chunk (27144 keys in 5 slots), and with
+  `--local_attn_size 17` the rolling part starts 1508 tokens into the older of its two chunks.
 """
 from .. import kernels
 
@@ -125,7 +127,13 @@ class QuantKVRing:
                 else:
                     out[0] = (s, a + drop, c - drop)
                     drop = 0
-        return out
+        merged = []   # a chunk the sink ends in and the rolling part starts in, without a gap: one range
+        for r in out:
+            if merged and merged[-1][0] == r[0] and merged[-1][1] + merged[-1][2] == r[1]:
+                merged[-1] = (r[0], merged[-1][1], merged[-1][2] + r[2])
+            else:
+                merged.append(r)
+        return merged
 
     def _begin_chunk(self, n):
         """Token window: take a slot for a new n-token chunk -- one holding no token the next window reads."""
@@ -183,35 +191,34 @@ class QuantKVRing:
         return self._ranges(self.lens[self.current])
 
     def attended(self):
-        """(slots, lengths) the attention reads: the sink chunks, the other saved chunks oldest first, then the
-        current chunk; each slot read from its first token."""
+        """(slots, lengths, first tokens) the attention reads, in order: the sink chunks, the other saved chunks
+        oldest first, then the current chunk; slot s read over tokens [first, first + length)."""
         ranges = self.attended_ranges()
-        if any(a != 0 for _, a, _ in ranges):
-            raise NotImplementedError("this window reads a chunk from past its first token; the attention kernel "
-                                      "reads chunk prefixes")
-        return [s for s, _, _ in ranges], [c for _, _, c in ranges]
+        return [s for s, _, _ in ranges], [c for _, _, c in ranges], [a for _, a, _ in ranges]
 
     def attend(self, q, layer, sm_scale=None):
         """Attention of q [B, Lq, H, 128] bf16 over the saved chunks plus the current one of `layer`."""
         b, lq, h, _ = q.shape
-        slots, lens = self.attended()
+        slots, lens, firsts = self.attended()
         if any(n == 0 for n in lens):
             raise RuntimeError("the current chunk has no K/V yet: call write() first")
         q8, qs, bias = kernels.quant_q(q, "NHD", self.cache, layer, slots)
         out = q.new_empty(q.shape)
-        return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale)
+        return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale,
+                                seg_firsts=firsts)
 
     def attend_projected(self, q, layer, norm_weight, rope, eps=1e-6, sm_scale=None):
         """attend() from the q projection [B, Lq, H * 128]: RMSNorm and the rotary embedding fused into the Q
         quantisation. Returns [B, Lq, H, 128] bf16."""
         b, lq = q.shape[0], q.shape[1]
         h = self.cache.heads
-        slots, lens = self.attended()
+        slots, lens, firsts = self.attended()
         if any(n == 0 for n in lens):
             raise RuntimeError("the current chunk has no K/V yet: call write() first")
         q8, qs, bias, _ = kernels.norm_rope_quant_q(q, h, norm_weight, eps, rope, self.cache, layer, slots)
         out = q.new_empty(b, lq, h, kernels.HEAD_DIM)
-        return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale)
+        return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale,
+                                seg_firsts=firsts)
 
     def commit(self):
         """The chunk is finished (its clean forward was written).

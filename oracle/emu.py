@@ -112,7 +112,7 @@ def _quant_int8_blocks(xf, blk):
 
 
 def quant_q(q):
-    """q bf16 [Lq, H, D] -> (q8 int8 [H, Lp, D], q_scale fp32 [H, Lp / 32]); Lp = Lq rounded up to 128."""
+    """q bf16 [Lq, H, D] -> (q8 int8 [H, Lp, D], q_scale fp32 [H, Lp / 32]); Lp = Lq rounded up to 256 (Q_TILE)."""
     q = _as_lhd(q)
     lq, h, d = q.shape
     lp = pad_to(lq, Q_TILE)
@@ -201,16 +201,26 @@ def requant(k, v):
     return {"k8": k8, "k_scale": ks, "km": km, "v8": v8, "v8lo": v8lo, "v_scale": vs, "n": k.shape[0]}
 
 
+def span(chunk):
+    """(first, n, first block, blocks) of the keys a quantised chunk is read over: keys [first, first + n) of its
+    slot ("first" defaults to 0; "n" is the count read), in the slot's own 64-key blocks, so the first block may
+    start before `first` and the last may end past first + n (those keys are masked)."""
+    first, n = chunk.get("first", 0), chunk["n"]
+    b0 = first // K_BLOCK
+    return first, n, b0, pad_to(first + n, K_BLOCK) // K_BLOCK - b0
+
+
 def dequant_v(chunk, terms=None):
-    """e4m3 V of a quantised chunk back to fp32 [H, n, D] in key order, without the V scale: hi + lo / 16
-    (or hi alone with terms=1, the default for a chunk whose "v8lo" is None)."""
+    """e4m3 V of a quantised chunk back to fp32 [H, first + n, D] in key order (slot keys 0 .. first + n - 1),
+    without the V scale: hi + lo / 16 (or hi alone with terms=1, the default for a chunk whose "v8lo" is None)."""
     if terms is None:   # a chunk quantised without the residual plane has one term
         terms = V_TERMS if chunk.get("v8lo") is not None else 1
     h, nb, d, _ = chunk["v8"].shape
+    end = chunk.get("first", 0) + chunk["n"]
     out = 0
     for bits, w in ((chunk["v8"], 1.0), (chunk["v8lo"], 1.0 / V_LO_SCALE))[:terms]:
         vals = e4m3_decode(bits)[:, :, :, torch.from_numpy(V_POS_OF_KEY)]   # [h, nb, d, key]
-        out = out + vals.permute(0, 1, 3, 2).reshape(h, nb * K_BLOCK, d)[:, :chunk["n"]] * w
+        out = out + vals.permute(0, 1, 3, 2).reshape(h, nb * K_BLOCK, d)[:, :end] * w
     return out
 
 
@@ -269,17 +279,17 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
     o = torch.zeros(rows, d)
     j = 0
     for ci, c in enumerate(chunks):
-        n = c["n"]
-        nbc = pad_to(n, K_BLOCK) // K_BLOCK
+        first, n, b0, nbc = span(c)
         if j + nbc <= j0 or j >= j1:
             j += nbc
             continue
         vs = c["v_scale"][hh]
         beta = beta_of(ci)
         for b in range(max(0, j0 - j), min(nbc, j1 - j)):
-            k0, k1 = b * K_BLOCK, min(n, b * K_BLOCK + K_BLOCK)
+            sb = b0 + b   # the slot's block
+            k0, k1 = max(first, sb * K_BLOCK), min(first + n, sb * K_BLOCK + K_BLOCK)
             s_int = torch.matmul(qf, c["k8"][hh, k0:k1].float().t())
-            cb = (qsr * sl2) * c["k_scale"][hh, b]
+            cb = (qsr * sl2) * c["k_scale"][hh, sb]
             m_blk = s_int.amax(dim=1) * cb + beta
             m_new = torch.where(m_blk > m_run + tau, m_blk, m_run)
             if stats is not None:
@@ -300,8 +310,9 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
 
 
 def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None, stats=None, p_round=True):
-    """Emulated quantized attention of q bf16 [Lq, H, D] over quantised chunks (dicts from `requant`), in the
-    kernel's own order: chunks in sequence, 64-key blocks in sequence, a reference row max m, and per block
+    """Emulated quantized attention of q bf16 [Lq, H, D] over quantised chunks (dicts from `requant`; a chunk is
+    read over keys [first, first + n) of its slot, see `span`), in the kernel's own order: chunks in sequence, the
+    slot's 64-key blocks in sequence (keys outside the read range masked), a reference row max m, and per block
       b = max_j S_ij * cb + beta,  m_new = b if b > m + tau else m,  alpha = exp2(m - m_new),
       o = alpha * o,  l = alpha * l,  P_ij = exp2(S_ij * cb + beta - m_new + 8.807 - tau)  (<= 448),
       l += sum P,  o += (e4m3(P) . V8) * v_scale,
@@ -321,7 +332,7 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
     multi = len(chunks) > 1
     vdec = [dequant_v(c) for c in chunks]
     bias = [q_bias(q, c["km"]) * sl2 if multi else None for c in chunks]
-    nb = sum(pad_to(c["n"], K_BLOCK) // K_BLOCK for c in chunks)
+    nb = sum(span(c)[3] for c in chunks)
     q_tiles = pad_to(lq, Q_TILE) // Q_TILE
     sched = attn_schedule(q_tiles * h, nb, schedule_gx) if schedule_gx else None
     out = torch.empty(lq, h, d, dtype=torch.float32)
@@ -376,9 +387,9 @@ def attention_exact_max(q, chunks, sm_scale=None, q_block=1024):
             qsr = qs[hh].repeat_interleave(Q_GROUP)[a:e]
             logits = []
             for ci, c in enumerate(chunks):
-                n = c["n"]
-                s_int = torch.matmul(q8[hh, a:e].float(), c["k8"][hh, :n].float().t())
-                ksr = c["k_scale"][hh].repeat_interleave(K_BLOCK)[:n]
+                first, n = c.get("first", 0), c["n"]
+                s_int = torch.matmul(q8[hh, a:e].float(), c["k8"][hh, first:first + n].float().t())
+                ksr = c["k_scale"][hh].repeat_interleave(K_BLOCK)[first:first + n]
                 s = s_int * ((qsr[:, None] * ksr[None, :]) * sl2)
                 if multi:
                     s = s + bias[ci][hh, a:e, None]
@@ -390,7 +401,7 @@ def attention_exact_max(q, chunks, sm_scale=None, q_block=1024):
                 p = torch.exp2(logits[ci] - m[:, None] + P_OFFSET)
                 den = den + p.sum(dim=1)
                 p8 = e4m3_decode(e4m3_encode(p))
-                num = num + torch.matmul(p8, vdec[ci][hh]) * c["v_scale"][hh][None, :]
+                num = num + torch.matmul(p8, vdec[ci][hh, c.get("first", 0):]) * c["v_scale"][hh][None, :]
             out[a:e, hh] = num / den[:, None]
     return out
 

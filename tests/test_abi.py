@@ -206,15 +206,18 @@ def test_quant_rows_fp8_argument_checks(lib):
         assert mx() == E_DEVICE
 
 
-def attn(lib, **kw):
+def attn(lib, logits=None, **kw):
     seg = (ctypes.c_int32 * 8)(0, 1, 2, 3, 0, 0, 0, 0)
     ln = (ctypes.c_int32 * 8)(128, 128, 128, 100, 0, 0, 0, 0)
     a = dict(q8=FAKE, qs=FAKE, bias=FAKE, batch=1, lq=100, heads=2, k8=FAKE, ks=FAKE, v8=FAKE, v8lo=None,
-             vs=FAKE, slots=4, cap=128, n_seg=4, seg=seg, ln=ln, out=FAKE, os=(0, 256, 128), sm=0.088, ws=FAKE)
+             vs=FAKE, slots=4, cap=128, n_seg=4, seg=seg, ln=ln, first=None, out=FAKE, os=(0, 256, 128), sm=0.088,
+             ws=FAKE)
     a.update(kw)
-    return lib.lbw_attn_fwd(a["q8"], a["qs"], a["bias"], a["batch"], a["lq"], a["heads"], a["k8"], a["ks"],
-                            a["v8"], a["v8lo"], a["vs"], a["slots"], a["cap"], a["n_seg"], a["seg"], a["ln"],
-                            a["out"], *a["os"], a["sm"], a["ws"], None)
+    args = (a["q8"], a["qs"], a["bias"], a["batch"], a["lq"], a["heads"], a["k8"], a["ks"], a["v8"], a["v8lo"],
+            a["vs"], a["slots"], a["cap"], a["n_seg"], a["seg"], a["ln"], a["first"], a["out"], *a["os"], a["sm"])
+    if logits is not None:   # the checking build: the same arguments plus the logits output
+        return lib.lbw_qk_logits_i32(*args, logits, a["ws"], None)
+    return lib.lbw_attn_fwd(*args, a["ws"], None)
 
 
 def test_attn_argument_checks(lib):
@@ -232,8 +235,16 @@ def test_attn_argument_checks(lib):
     assert attn(lib, os=(0, 256, 130)) == E_ALIGN
     assert attn(lib, out=FAKE + 2) == E_ALIGN
     assert attn(lib, v8=FAKE + 8) == E_ALIGN
-    assert lib.lbw_qk_logits_i32(FAKE, 2, 100, None, 1, 128, 0, FAKE, None) == E_NULL
-    assert lib.lbw_qk_logits_i32(FAKE, 2, 100, FAKE, 1, 128, 1, FAKE, None) == E_SHAPE
+    # first tokens: a chunk read from token `first` must end inside its slot
+    first = lambda *f: (ctypes.c_int32 * 8)(*f, *[0] * (8 - len(f)))  # noqa: E731
+    assert attn(lib, first=first(0, 0, 0, 29)) == E_SEGMENTS          # 29 + 100 > 128
+    assert attn(lib, first=first(0, -1, 0, 0)) == E_SEGMENTS
+    assert attn(lib, first=first(0, 0, 1, 0)) == E_SEGMENTS           # 1 + 128 > 128
+    # the checking build takes the same checks, and its logits output
+    assert attn(lib, logits=FAKE, q8=None) == E_NULL
+    assert attn(lib, logits=0) == E_NULL                                # a null logits pointer
+    assert attn(lib, logits=FAKE + 2) == E_ALIGN
+    assert attn(lib, logits=FAKE, first=first(0, 0, 0, 29)) == E_SEGMENTS
 
 
 def hip_device_count():
@@ -269,9 +280,11 @@ def test_valid_call_without_gfx950_is_refused(lib):
     assert lib.lbw_cross_prepare(FAKE, FAKE, 1, 512, 2, 0, 256, 128, 0, 256, 128, FAKE, FAKE, None) == E_DEVICE
     seg = (ctypes.c_int32 * 1)(0)
     ln = (ctypes.c_int32 * 1)(100)
+    first = (ctypes.c_int32 * 1)(28)
     assert lib.lbw_attn_fwd_noalloc(FAKE, FAKE, None, 1, 100, 2, FAKE, FAKE, FAKE, None, FAKE, 1, 128, 1, seg, ln,
-                                    FAKE, 0, 256, 128, 0.088, None) == E_DEVICE
-    assert lib.lbw_qk_logits_i32(FAKE, 2, 100, FAKE, 1, 128, 0, FAKE, None) == E_DEVICE
+                                    first, FAKE, 0, 256, 128, 0.088, None) == E_DEVICE
+    assert attn(lib, first=(ctypes.c_int32 * 8)(0, 0, 0, 28, 0, 0, 0, 0)) == E_DEVICE
+    assert attn(lib, logits=FAKE) == E_DEVICE
 
 
 def test_loader_fails_loudly_without_library(tmp_path, monkeypatch):

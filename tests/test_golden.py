@@ -57,7 +57,8 @@ def test_hip_matches_fixtures(gold):
     ring = kernels.RingCache(1, 1, h, 128, 1, DEV)
     kernels.kv_requant(gold["k"].to(DEV), gold["v"].to(DEV), ring, 0)
     q8, qs, _ = kernels.quant_q(gold["q"].to(DEV))
-    logits = kernels.qk_logits(q8, 70, ring, 0, 0)
+    raw, _ = kernels.qk_logits(q8, qs, None, 1, 70, h, ring, 0, [0], [100])
+    logits = raw - kernels.S_MAGIC   # the attention kernel's accumulator words, less their start value
     torch.cuda.synchronize()
     assert np.array_equal(ring.km[0, 0].cpu().numpy(), gold["km"])
     assert np.array_equal(ring.v_scale[0, 0].cpu().numpy(), gold["v_scale"])

@@ -122,21 +122,94 @@ def test_quant_q_bit_exact(lq):
     torch.testing.assert_close(qs.cpu(), rs, rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("lq,lk", [(128, 64), (200, 130), (1508, 1508)])
-def test_qk_logits_bit_exact(lq, lk):
-    torch.manual_seed(lq + lk)
-    h = 2
-    q = torch.randn(1, lq, h, 128).to(torch.bfloat16)
-    k = (torch.randn(1, lk, h, 128) + 3 * torch.randn(1, 1, h, 128)).to(torch.bfloat16)
-    ring = _ring(1, h, lk)
-    _k().kv_requant(k.to(DEV), k.to(DEV), ring, 0)
-    q8, _, _ = _k().quant_q(q.to(DEV))
-    s = _k().qk_logits(q8, lq, ring, 0, 0)
+def _raw_logits_ref(q, parts):
+    """The words the attention kernel's checking build writes: for each chunk read over [first, first + n) of its
+    slot (oracle k8 of the whole slot), every 64-key slot block the range touches, S_MAGIC + q8 . k8 in int32."""
+    q8, _ = emu.quant_q(q)
+    cols = []
+    for k8, first, n in parts:
+        b0, b1 = first // 64, (first + n + 63) // 64
+        cols.append(emu.qk_logits(q8, k8[:, 64 * b0:64 * b1]))
+    return torch.cat(cols, dim=2) + _k().S_MAGIC
+
+
+@pytest.mark.parametrize("case", ["cfg1", "ring"])
+def test_attention_kernel_logits_bit_exact(case):
+    """BASELINE's int32-logit gate on the attention kernel itself: its checking build (the same DMA stages, XOR
+    swizzle, fragment reads and 1/(2 pi) accumulator start, plus a store of each block's accumulator words) gives
+    S_MAGIC + q8 . k8 bit for bit against the oracle's int64-pinned logits, at cfg 1 (1508 x 1508, 12 heads) and on
+    a 4-chunk ring read over windows that start and end inside 64-key blocks, with every tile cut into pieces. The
+    words read as floats are exactly 1/(2 pi) + S * 2^-26, and the checking build's output equals the production
+    call's bit for bit."""
+    k = _k()
+    if case == "cfg1":
+        h, lq = 12, 1508
+        q, kk, vv, _ = emu.make_inputs(lq, 1508, h=h)
+        data, firsts, lens = [(kk, vv)], [0], [1508]
+    else:
+        h, lq = 3, 300
+        g = torch.Generator().manual_seed(55)
+        data = [((torch.randn(1, n, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16(),
+                 torch.randn(1, n, h, 128, generator=g).bfloat16()) for n in (700, 333, 65, 129)]
+        q = torch.randn(1, lq, h, 128, generator=g).bfloat16()
+        firsts, lens = [37, 0, 10, 64], [663, 333, 55, 65]
+    cap = k.pad_to(max(d[0].shape[1] for d in data), 64)
+    ring = k.RingCache(1, 1, h, cap, len(data), DEV)
+    for i, (kk, vv) in enumerate(data):
+        k.kv_requant(kk.to(DEV), vv.to(DEV), ring, i)
+    slots = list(range(len(data)))
+    q8, qs, bias = k.quant_q(q.to(DEV), "NHD", ring, 0, slots)
+    raw, out = k.qk_logits(q8, qs, bias, 1, lq, h, ring, 0, slots, lens, firsts)
+    prod = torch.empty_like(out)
+    k.attn_fwd(q8, qs, bias, 1, lq, h, ring, 0, slots, lens, prod, seg_firsts=firsts)
     torch.cuda.synchronize()
-    r8, _ = emu.quant_q(q)
-    rk = emu.requant(k, k)
-    ref = emu.qk_logits(r8, rk["k8"])
-    assert torch.equal(s.cpu()[:, :, :ref.shape[2]], ref)
+    raw = raw.cpu()
+    ref = _raw_logits_ref(q, [(emu.requant(kk, vv)["k8"], a, n) for (kk, vv), a, n in zip(data, firsts, lens)])
+    assert raw.shape == ref.shape and torch.equal(raw, ref)
+    magic_f = torch.tensor([k.S_MAGIC], dtype=torch.int32).view(torch.float32).double()
+    assert torch.equal((raw.view(torch.float32).double() - magic_f) * 2.0 ** 26, (raw - k.S_MAGIC).double())
+    assert torch.equal(out, prod)
+    record(f"int32 QK^T logits of the attention kernel ({case}: {raw.numel()} words, {len(data)} chunk(s)) "
+           f"bit-exact vs the oracle; checking build output == production output")
+
+
+def test_chunk_ranges_vs_oracle():
+    """Chunks read over explicit ranges of their slots: a suffix from inside a block, a middle range inside one
+    block (both of its masks), a one-key range at a block's last key and one at the next block's first, a range
+    from a block boundary, a prefix and a whole chunk -- against the oracle over exactly those keys and fp32 SDPA."""
+    k = _k()
+    h, lq = 2, 300
+    g = torch.Generator().manual_seed(57)
+    lens_q = (333, 200, 128, 130, 256, 90, 150)
+    data = [((torch.randn(1, n, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16(),
+             (torch.randn(1, n, h, 128, generator=g) * (1 + 0.3 * i)).bfloat16()) for i, n in enumerate(lens_q)]
+    q = torch.randn(1, lq, h, 128, generator=g).bfloat16()
+    ranges = [(37, 296), (70, 20), (63, 1), (64, 1), (128, 128), (0, 50), (0, 150)]
+    ring = k.RingCache(1, 1, h, 384, len(data), DEV)
+    for i, (kk, vv) in enumerate(data):
+        k.kv_requant(kk.to(DEV), vv.to(DEV), ring, i)
+    slots = list(range(len(data)))
+    firsts, lens = [a for a, _ in ranges], [n for _, n in ranges]
+    q8, qs, bias = k.quant_q(q.to(DEV), "NHD", ring, 0, slots)
+    out = torch.empty(1, lq, h, 128, dtype=torch.bfloat16, device=DEV)
+    k.attn_fwd(q8, qs, bias, 1, lq, h, ring, 0, slots, lens, out, seg_firsts=firsts)
+    out = out.float().cpu()
+    chunks = []
+    for (kk, vv), (a, n) in zip(data, ranges):
+        c = emu.requant(kk, vv)
+        c["first"], c["n"] = a, n
+        chunks.append(c)
+    ref = emu.attention(q, chunks, schedule_gx=_gx())[None]
+    kcat = torch.cat([kk[:, a:a + n] for (kk, _), (a, n) in zip(data, ranges)], 1)
+    vcat = torch.cat([vv[:, a:a + n] for (_, vv), (a, n) in zip(data, ranges)], 1)
+    sd = emu.sdpa_fp32(q, kcat, vcat)[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    record(f"chunk ranges from mid-block (7 chunks, {kcat.shape[1]} keys) vs oracle mean {e_emu.mean():.3e}; "
+           f"vs fp32 SDPA max {e_sd.max():.3e} mean {e_sd.mean():.3e}; oracle vs SDPA mean {e_scheme.mean():.3e}")
+    assert torch.isfinite(out).all()
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
+    assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
 
 
 def _gx():
@@ -333,7 +406,7 @@ def test_memory_ring_many_short_chunks():
         ring.write(0, kk.to(DEV), vv.to(DEV))
         ring.commit()
     ring.write(0, ks[-1].to(DEV), vs[-1].to(DEV))
-    slots, seg = ring.attended()
+    slots, seg, _ = ring.attended()
     assert [int(x) for x in seg] == list(lens), (slots, seg)
     out = ring.attend(q.to(DEV), 0).float().cpu()
     ref = emu.attention(q, [emu.requant(kk, vv) for kk, vv in zip(ks, vs)], schedule_gx=_gx())[None]
@@ -345,6 +418,32 @@ def test_memory_ring_many_short_chunks():
     assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
     assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
     assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
+
+
+def test_sage_kvq_surface():
+    """The reference's sage_kvq call surface (alloc_cache(shape, dtype, device), requant_all, write_chunk,
+    attend(q, cache, kv_len, sm_scale); experiments/modules/sage_kvq.py:38-111) over a layer cache dict holding the
+    bf16 window: attend() equals the drop-in sage_attention over the same slice bit for bit, after requant_all and
+    after a write_chunk that extends the slice; release() drops the quantised buffers."""
+    from lingbot_world_v2_realtime_amd import sage_attention
+    from lingbot_world_v2_realtime_amd.layers import sage_kvq
+    h, kv = 3, 700
+    g = torch.Generator().manual_seed(71)
+    cache = {"k": (torch.randn(1, kv, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16(),
+             "v": torch.randn(1, kv, h, 128, generator=g).bfloat16()}
+    q = torch.randn(1, 300, h, 128, generator=g).bfloat16().to(DEV)
+    cache = {key: t.to(DEV) for key, t in cache.items()}
+    cache.update(sage_kvq.alloc_cache(cache["k"].shape, torch.bfloat16, DEV))
+    sage_kvq.requant_all(cache, 450)
+    got = sage_kvq.attend(q, cache, 450)
+    want = sage_attention(q, cache["k"][:, :450], cache["v"][:, :450])
+    sage_kvq.write_chunk(cache, 450, kv)
+    got2 = sage_kvq.attend(q, cache, kv, sm_scale=0.07)
+    want2 = sage_attention(q, cache["k"], cache["v"], sm_scale=0.07)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(got2, want2)
+    sage_kvq.release([cache])
+    assert set(cache) == {"k", "v"}
 
 
 def test_hnd_layout_same_bits():
@@ -575,8 +674,8 @@ def test_reference_window_ring():
             ring.commit()
     pos = ring.stream_positions()
     assert pos == kv_window.rollout_positions([n] * 7, 1, 18 * frame, 6 * frame)[6][0].tolist()
-    slots, lens = ring.attended()
-    assert lens == [200, 100, 200, 200, 200]
+    slots, lens, firsts = ring.attended()
+    assert lens == [200, 100, 200, 200, 200] and firsts == [0] * 5
     out = ring.attend(q.to(DEV), 0).float().cpu()
     used = [(0, 200), (1, 100), (4, 200), (5, 200), (6, 200)]
     ref_chunks = []
@@ -595,6 +694,81 @@ def test_reference_window_ring():
     assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
     assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
     assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
+
+
+def _window_rollout(h, frame, local, n_chunks, q_len, seed, max_attention_size=None, sink=6, mem_scale=1.0):
+    """A rollout of 4-frame chunks through the reference's token window: (ring after writing the last chunk, the
+    chunks' bf16 K/V, q, and the attended (chunk index, first token, tokens) ranges)."""
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    n = 4 * frame
+    g = torch.Generator().manual_seed(seed)
+    chunks = [((torch.randn(1, n, h, 128, generator=g) + 2 * torch.randn(1, 1, h, 128, generator=g)).bfloat16(),
+               (torch.randn(1, n, h, 128, generator=g) * (mem_scale if i < n_chunks - 1 else 1.0)).bfloat16())
+              for i in range(n_chunks)]
+    q = torch.randn(1, q_len, h, 128, generator=g).bfloat16()
+    ring = QuantKVRing.from_frames(1, 1, h, frame, 4, sink, local, device=DEV, max_attention_size=max_attention_size)
+    for i, (kk, vv) in enumerate(chunks):
+        ring.write(0, kk.to(DEV), vv.to(DEV))
+        if i < n_chunks - 1:
+            ring.commit()
+    chunk_of = {slot: pos // n for slot, pos, _ in ring.saved}
+    chunk_of[ring.current] = n_chunks - 1
+    slots, lens, firsts = ring.attended()
+    used = [(chunk_of[s], a, m) for s, m, a in zip(slots, lens, firsts)]
+    assert ring.stream_positions() == [i * n + a + t for i, a, m in used for t in range(m)]
+    return ring, chunks, q, used
+
+
+@pytest.mark.parametrize("local,mas,want", [
+    (17, None, [(0, 0, 200), (1, 0, 100), (5, 50, 150), (6, 0, 200), (7, 0, 200)]),   # rolling part from token 50
+    (18, 650, [(1, 50, 50), (5, 0, 200), (6, 0, 200), (7, 0, 200)]),                  # the trim cuts the sink
+])
+def test_window_mid_chunk_ring(local, mas, want):
+    """The reference's token window where a chunk is read from inside it (kv_cache.py:23-81): --local_attn_size 17
+    with sink 6 (850 keys, the rolling part starting 50 tokens into a chunk, a masked lead in its first block), and
+    --local_attn_size 18 trimmed by max_attention_size 650 (the sink's second chunk read over tokens 50..99, one
+    block with both masks) at 50-token frames -- against the oracle over exactly those tokens and fp32 SDPA."""
+    from oracle import kv_window
+    h, frame = 3, 50
+    ring, chunks, q, used = _window_rollout(h, frame, local, 8, 250, seed=68 + local, max_attention_size=mas)
+    assert used == want, used
+    pos = kv_window.rollout_positions([4 * frame] * 8, 1, local * frame, 6 * frame,
+                                      max_attention_size=mas or 1_000_000)[7][0].tolist()
+    assert ring.stream_positions() == pos
+    out = ring.attend(q.to(DEV), 0).float().cpu()
+    ref_chunks = []
+    for i, a, m in used:
+        c = emu.requant(*chunks[i])
+        c["first"], c["n"] = a, m
+        ref_chunks.append(c)
+    ref = emu.attention(q, ref_chunks, schedule_gx=_gx())[None]
+    kk = torch.cat([chunks[i][0][:, a:a + m] for i, a, m in used], 1)
+    vv = torch.cat([chunks[i][1][:, a:a + m] for i, a, m in used], 1)
+    sd = emu.sdpa_fp32(q, kk, vv)[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    record(f"window local {local} max_attention_size {mas} ({kk.shape[1]} keys, reads from mid-chunk) vs oracle "
+           f"mean {e_emu.mean():.3e}; vs fp32 SDPA max {e_sd.max():.3e} mean {e_sd.mean():.3e}; oracle vs SDPA "
+           f"mean {e_scheme.mean():.3e}")
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
+    assert e_sd.max() <= 2 * e_scheme.max() + 1e-3
+
+
+def test_window_local17_full_size():
+    """--sink_size 6 --local_attn_size 17 at the real shape (1508-token frames, 4-frame chunks, 12 heads): chunk 6
+    attends chunk 0, the first 3016 tokens of chunk 1, chunk 4 from token 1508, chunk 5 and itself (6032 q x 25636
+    keys), within the BASELINE gates of fp32 SDPA over exactly those bf16 keys."""
+    ring, chunks, q, used = _window_rollout(12, 1508, 17, 7, 6032, seed=69)
+    assert used == [(0, 0, 6032), (1, 0, 3016), (4, 1508, 4524), (5, 0, 6032), (6, 0, 6032)], used
+    out = ring.attend(q.to(DEV), 0).float()
+    kk = torch.cat([chunks[i][0][:, a:a + m] for i, a, m in used], 1)
+    vv = torch.cat([chunks[i][1][:, a:a + m] for i, a, m in used], 1)
+    sd = _sdpa_gpu_fp32(q, kk, vv)
+    e = (out - sd).abs()
+    msg = (f"window local 17 full size (6032 q x {kk.shape[1]} keys, chunk 4 read from token 1508) vs fp32 SDPA: "
+           f"max {e.max():.3e} (gate {SDPA_MAX_ABS:g}) mean {e.mean():.3e} (gate {SDPA_MEAN_ABS:g})")
+    record(msg)
+    assert e.max() < SDPA_MAX_ABS and e.mean() < SDPA_MEAN_ABS, msg
 
 
 def test_cfg5_chunk_graph_full_size():

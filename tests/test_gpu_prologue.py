@@ -118,6 +118,28 @@ def test_norm_rope_kv_requant_bit_exact(n, heads, grid_hw, start):
     _check_slot(ring, 1, 0, ref, n)
 
 
+def test_prologue_eps_zero_ragged():
+    """eps = 0 (the ABI takes it) with lengths that end inside a 32-row group: the padding rows must stay exact
+    zeros (1 / sqrt(0 + 0) would make them NaN and spread into the Q scale and the chunk's K mean), so the int8 Q,
+    its scales, the roped K and every ring field stay bit-exact against the oracle, which pads with zeros."""
+    k = _k()
+    heads, grid_hw = 2, (5, 7)
+    for n in (45, 100):
+        x = _rows(1, n, heads, 300 + n)
+        w = _weight(heads, 13)
+        q8, qs, _, roped = k.norm_rope_quant_q(x.to(DEV), heads, w.to(DEV), 0.0, _rope(grid_hw, 1), want_roped=True)
+        v = (torch.randn(1, n, heads, 128) * 1.3).to(torch.bfloat16)
+        ring = k.RingCache(1, 1, heads, k.pad_to(n, 64), 1, DEV)
+        k_out = k.norm_rope_kv_requant(x.to(DEV), v.to(DEV), heads, w.to(DEV), 0.0, _rope(grid_hw, 1), ring, 0)
+        torch.cuda.synchronize()
+        ref = torch.stack([pro.norm_rope(x[0], w, 0.0, heads, pro.rope_table(), grid_hw, 1)])
+        assert torch.equal(roped.cpu(), ref) and torch.equal(k_out.cpu(), ref)
+        r8, rs = emu.quant_q(ref[0])
+        assert torch.equal(q8.cpu(), r8) and torch.equal(qs.cpu(), rs)
+        _check_slot(ring, 0, 0, emu.requant(ref[0], v[0]), n)
+        assert torch.isfinite(ring.km[0, 0]).all()
+
+
 def _sdpa_gpu_fp32(q, k, v):
     """fp32 softmax attention on the GPU, per head: [L, H, D] -> fp32 [Lq, H, D]."""
     qd, kd, vd = (x.to(DEV).float() for x in (q, k, v))
@@ -157,8 +179,8 @@ def test_full_chunk_from_projections():
         roped_k.append(_oracle_roped(kk, wk, heads, (29, 52), c * frames)[0])
         vs.append(v[0])
     torch.cuda.synchronize()
-    slots, lens = ring.attended()
-    assert lens == [n, 3016, n, n, n]
+    slots, lens, firsts = ring.attended()
+    assert lens == [n, 3016, n, n, n] and firsts == [0] * 5
     _check_slot(ring.cache, 0, slots[-1], emu.requant(roped_k[4], vs[4]), n)
     rq = _oracle_roped(q, wq, heads, (29, 52), 4 * frames)[0]
     used = [(0, n), (1, 3016), (2, n), (3, n), (4, n)]

@@ -31,7 +31,8 @@ def test_ring_slot_rotation():
     seen = []
     for chunk in range(7):
         ring.lens[ring.current] = 100 - chunk        # what write() records
-        slots, lens = ring.attended()
+        slots, lens, firsts = ring.attended()
+        assert firsts == [0] * len(slots)
         seen.append((slots, lens))
         assert slots[-1] == ring.current and len(set(slots)) == len(slots)
         ring.commit()

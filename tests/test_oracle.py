@@ -315,13 +315,13 @@ def _direct_softmax_fp64(q, chunks, sm_scale=None):
     for hh in range(h):
         logits, vals = [], []
         for c in chunks:
-            n = c["n"]
-            s = q8[hh, :lq].double() @ c["k8"][hh, :n].double().t()
-            s = s * qsr[hh, :lq, None] * c["k_scale"][hh].repeat_interleave(emu.K_BLOCK)[:n].double()[None, :]
+            a, n = c.get("first", 0), c["n"]
+            s = q8[hh, :lq].double() @ c["k8"][hh, a:a + n].double().t()
+            s = s * qsr[hh, :lq, None] * c["k_scale"][hh].repeat_interleave(emu.K_BLOCK)[a:a + n].double()[None, :]
             if len(chunks) > 1:
                 s = s + (q[:, hh].double() @ c["km"][hh].double())[:, None]
             logits.append(s * sm)
-            vals.append(emu.dequant_v(c)[hh].double() * c["v_scale"][hh].double()[None, :])
+            vals.append(emu.dequant_v(c)[hh, a:a + n].double() * c["v_scale"][hh].double()[None, :])
         s = torch.cat(logits, dim=1)
         p = torch.softmax(s, dim=1)
         out[:, hh] = p @ torch.cat(vals, dim=0)
@@ -342,6 +342,28 @@ def test_online_split_and_chunk_switch_exact_without_p_rounding(gx):
         assert any(len(p) > 1 for p in sched.values()) == (gx > 1)
     err = (got - want).abs().max().item()
     assert err < 2e-5 * want.abs().max().item(), err
+
+
+@pytest.mark.parametrize("gx", [None, 2, 16])
+def test_windows_read_from_mid_chunk_exact_without_p_rounding(gx):
+    """Chunks read over a window of their keys, as the token window reads them: a suffix from a key inside a
+    64-key block (the leading keys of that block masked), a middle range whose first and last keys share one
+    block, a suffix from a block boundary, and a whole chunk. With P unrounded the oracle must equal direct
+    softmax attention over exactly those keys: a wrong block offset, K-scale index or mask edge is an O(1)
+    error for the keys it moves."""
+    q, ks, vs = _ragged_chunks(34, lens=(333, 200, 256, 150))
+    chunks = [emu.requant(k, v) for k, v in zip(ks, vs)]
+    for c, (first, n) in zip(chunks, ((37, 296), (70, 50), (128, 128), (0, 150))):
+        c["first"], c["n"] = first, n
+    assert [emu.span(c)[2:] for c in chunks] == [(0, 6), (1, 1), (2, 2), (0, 3)]
+    want = _direct_softmax_fp64(q, chunks)
+    got = emu.attention(q, chunks, schedule_gx=gx, p_round=False).double()
+    err = (got - want).abs().max().item()
+    assert err < 2e-5 * want.abs().max().item(), err
+    # the check can see an off-by-one: the same window shifted by one key moves the direct result past the bound
+    moved = [dict(c) for c in chunks]
+    moved[0]["first"] = 36
+    assert (_direct_softmax_fp64(q, moved) - want).abs().max() > 1e-3
 
 
 def test_split_pieces_change_only_p_rounding():

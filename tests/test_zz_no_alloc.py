@@ -21,9 +21,9 @@ def _case(lq, lk, h, seed, mem_chunks):
         ring.write(0, mk.to(DEV), mv.to(DEV))
         ring.commit()
     ring.write(0, k.to(DEV), v.to(DEV))
-    slots, lens = ring.attended()
+    slots, lens, firsts = ring.attended()
     q8, qs, bias = kernels.quant_q(q.to(DEV), "NHD", ring.cache, 0, slots)
-    return q8, qs, bias, ring, slots, lens
+    return q8, qs, bias, ring, slots, lens, firsts
 
 
 def test_noalloc_matches_workspace_call_twice():
@@ -32,11 +32,11 @@ def test_noalloc_matches_workspace_call_twice():
     for lq, lk, h, mem in ((1508, 1508, 6, 0), (300, 200, 2, 2)):
         tiles = kernels.pad_to(lq, kernels.Q_TILE) // kernels.Q_TILE * h
         assert tiles // 8 + 1 < gx             # no XCD has a whole tile per workgroup: every tile is split
-        q8, qs, bias, ring, slots, lens = _case(lq, lk, h, seed=lq + h, mem_chunks=mem)
+        q8, qs, bias, ring, slots, lens, firsts = _case(lq, lk, h, seed=lq + h, mem_chunks=mem)
         want = torch.empty(1, lq, h, 128, dtype=torch.bfloat16, device=DEV)
         got = torch.full_like(want, float("nan"))
-        kernels.attn_fwd(q8, qs, bias, 1, lq, h, ring.cache, 0, slots, lens, want)
-        kernels.attn_fwd(q8, qs, bias, 1, lq, h, ring.cache, 0, slots, lens, got, noalloc=True)
+        kernels.attn_fwd(q8, qs, bias, 1, lq, h, ring.cache, 0, slots, lens, want, seg_firsts=firsts)
+        kernels.attn_fwd(q8, qs, bias, 1, lq, h, ring.cache, 0, slots, lens, got, noalloc=True, seg_firsts=firsts)
         torch.cuda.synchronize()
         print(f"noalloc lq={lq} lk={lk} h={h} chunks={len(slots)}: bit-identical {torch.equal(got, want)}",
               flush=True)
