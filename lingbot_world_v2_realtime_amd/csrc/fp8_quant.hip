@@ -41,31 +41,53 @@ __device__ __forceinline__ float div_sc(float x, float sc, float r) {
   return __builtin_copysignf(fmaf(fmaf(-q, sc, x), r, q), x);
 }
 
-// e4m3 of 8 values divided by the row scale, as 8 bytes; x / scale is within 448 up to its own rounding, and the
-// clamp keeps a rounding above 448 off the overflow path
+// e4m3 of 8 values divided by the row scale, as 8 bytes. For a finite scale, |x / scale| <= 448 (1 + 2^-23) by
+// construction (|x| <= amax, scale >= amax / 448 up to its rounding), which the round-to-nearest cast takes to 448,
+// so no clamp is needed, and a NaN quotient stays NaN as the reference's cast makes it. A row holding an infinity
+// has scale = inf and r = 0: the quotient is then x * 0, +-0 for finite x and NaN for an infinite one, as IEEE
+// division by infinity gives (the correction step would turn 0 * inf into NaN); a NaN row has scale NaN and every
+// quotient NaN. (The row-uniform branch costs nothing.)
 __device__ __forceinline__ uint2 quant8(const float* f, float sc, float r) {
   uint32_t w[2];
+  const bool finite = sc < INFINITY;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    const float y0 = fminf(fmaxf(div_sc(f[4 * h], sc, r), -FP8_MAX), FP8_MAX);
-    const float y1 = fminf(fmaxf(div_sc(f[4 * h + 1], sc, r), -FP8_MAX), FP8_MAX);
-    const float y2 = fminf(fmaxf(div_sc(f[4 * h + 2], sc, r), -FP8_MAX), FP8_MAX);
-    const float y3 = fminf(fmaxf(div_sc(f[4 * h + 3], sc, r), -FP8_MAX), FP8_MAX);
-    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-    pk = __builtin_amdgcn_cvt_pk_fp8_f32(y2, y3, pk, true);
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = finite ? div_sc(f[4 * h + e], sc, r) : f[4 * h + e] * r;
+    int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    pk = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], pk, true);
     w[h] = (uint32_t)pk;
   }
   return make_uint2(w[0], w[1]);
 }
 
-// the row's amax over the workgroup (in every thread) -> its scale, written by thread 0
-__device__ __forceinline__ float row_scale(float amax, float* s_red, float* scale, int64_t row) {
+// |x| as bits: for non-negative floats the unsigned integer order is the float order, with every NaN above +inf,
+// so an integer max over these is an amax that propagates NaN (as torch's amax does; fmaxf would drop it)
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, dpp_u32<DPP_XOR1>(x));
+  x = max(x, dpp_u32<DPP_XOR2>(x));
+  x = max(x, dpp_u32<DPP_HALF_MIRROR>(x));
+  x = max(x, dpp_u32<DPP_MIRROR>(x));
+  auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  x = max((uint32_t)r[0], (uint32_t)r[1]);
+  r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return max((uint32_t)r[0], (uint32_t)r[1]);
+}
+
+// the row's amax (as abs_bits, over the workgroup, in every thread) -> its scale, written by thread 0:
+// max(amax / 448, 1e-12), NaN for a row holding a NaN and inf for one holding an infinity (the reference's clamp
+// keeps both)
+__device__ __forceinline__ float row_scale(uint32_t amax_bits, uint32_t* s_red, float* scale, int64_t row) {
   const int t = threadIdx.x;
-  amax = wave_max(amax);
-  if ((t & 63) == 0) s_red[t >> 6] = amax;
+  amax_bits = wave_max_u32(amax_bits);
+  if ((t & 63) == 0) s_red[t >> 6] = amax_bits;
   __syncthreads();
-  amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  const float sc = fmaxf(__fdiv_rn(amax, FP8_MAX), FP8_SCALE_FLOOR);
+  const float amax = __uint_as_float(max(max(s_red[0], s_red[1]), max(s_red[2], s_red[3])));
+  const float q = __fdiv_rn(amax, FP8_MAX);
+  const float sc = q < FP8_SCALE_FLOOR ? FP8_SCALE_FLOOR : q;
   if (t == 0) scale[row] = sc;
   return sc;
 }
@@ -74,12 +96,12 @@ __device__ __forceinline__ float row_scale(float amax, float* s_red, float* scal
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict__ x, int64_t cols, int64_t s_row,
                                                              uint8_t* __restrict__ x8, float* __restrict__ scale) {
-  __shared__ float s_red[4];
+  __shared__ uint32_t s_red[4];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * s_row;
   const int t = threadIdx.x;
   float f[NCH][8];
-  float amax = 0.f;
+  uint32_t amax = 0;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
     const int64_t c = 8 * (int64_t)(t + 256 * i);
@@ -90,7 +112,7 @@ __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict
       for (int e = 0; e < 8; ++e) f[i][e] = 0.f;
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[i][e]));
+    for (int e = 0; e < 8; ++e) amax = max(amax, abs_bits(f[i][e]));
   }
   const float sc = row_scale(amax, s_red, scale, row);
   const float r = __fdiv_rn(1.f, sc);
@@ -107,16 +129,16 @@ template <typename T>
 __global__ __launch_bounds__(256) void quant_rows_fp8_long_kernel(const T* __restrict__ x, int64_t cols,
                                                                   int64_t s_row, uint8_t* __restrict__ x8,
                                                                   float* __restrict__ scale) {
-  __shared__ float s_red[4];
+  __shared__ uint32_t s_red[4];
   const int64_t row = blockIdx.x;
   const T* xr = x + row * s_row;
   const int t = threadIdx.x;
-  float amax = 0.f;
+  uint32_t amax = 0;
   for (int64_t c = 8 * (int64_t)t; c < cols; c += 8 * 256) {
     float f[8];
     Row8<T>::load(xr + c, f);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
+    for (int e = 0; e < 8; ++e) amax = max(amax, abs_bits(f[e]));
   }
   const float sc = row_scale(amax, s_red, scale, row);
   const float r = __fdiv_rn(1.f, sc);
@@ -150,8 +172,10 @@ static void launch_quant_rows(const T* x, int64_t rows, int64_t cols, int64_t s_
 // MXFP8 (the reference's MXFP8Linear, lingbot/layers/linear.py:42-50): per 32 consecutive values of a row,
 // scale = 2^e with e = ceil(log2(max(amax, 2^-126) / 448)) taken exactly from the bits of the fp32 quotient
 // (floored at -127, E8M0's smallest), values e4m3(x / scale) (exact division by a power of two, then round to
-// nearest even), and the E8M0 byte e + 127. One thread per 32-value group; rows from `rows` up to `rows_pad` are
-// written as zeros with scale byte 127 (2^0), so the GEMM can take a row count padded to its tile.
+// nearest even), and the E8M0 byte e + 127. A group holding a NaN or an infinity gets what the reference's formula
+// gives it: the E8M0 NaN byte 255 and x / amax (all NaN for a NaN group; +-0, and NaN for the infinity, for an
+// infinite one). One thread per 32-value group; rows from `rows` up to `rows_pad` are written as zeros with scale
+// byte 127 (2^0), so the GEMM can take a row count padded to its tile.
 template <typename T>
 __global__ __launch_bounds__(256) void quant_mx_fp8_kernel(const T* __restrict__ x, int64_t rows, int64_t rows_pad,
                                                            int64_t cols, int64_t s_row, uint8_t* __restrict__ x8,
@@ -171,10 +195,11 @@ __global__ __launch_bounds__(256) void quant_mx_fp8_kernel(const T* __restrict__
   const T* xr = x + row * s_row + grp * 32;
 #pragma unroll
   for (int i = 0; i < 4; ++i) Row8<T>::load(xr + 8 * i, f + 8 * i);
-  float amax = 0.f;
+  uint32_t abits = 0;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(f[i]));
-  amax = fmaxf(amax, 0x1p-126f);
+  for (int i = 0; i < 32; ++i) abits = max(abits, abs_bits(f[i]));
+  const bool finite = abits < 0x7F800000u;
+  const float amax = fmaxf(__uint_as_float(finite ? abits : 0u), 0x1p-126f);
   const float qv = __fdiv_rn(amax, FP8_MAX);
   // exact ceil(log2(qv)) of a positive float: the exponent of its top bit, plus one unless qv is a power of two
   const uint32_t qb = __float_as_uint(qv);
@@ -187,21 +212,19 @@ __global__ __launch_bounds__(256) void quant_mx_fp8_kernel(const T* __restrict__
     e = (int)(qb >> 23) - 127 + ((qb & 0x7FFFFFu) ? 1 : 0);
   }
   e = e < -127 ? -127 : e;
-  // 1 / 2^e as a float (2^-e, e in [-127, 127]); x * 2^-e is exact for every finite x here
-  const float inv = e >= -126 ? __uint_as_float((uint32_t)(127 - e) << 23) : 0x1p127f;
-  e8[id] = (uint8_t)(e + 127);
+  // 1 / 2^e as a float (2^-e, e in [-127, 127]); x * 2^-e is exact for every finite x here, and |x| 2^-e <= 448
+  // (2^e >= amax / 448), so the cast needs no clamp. Non-finite group: 1 / amax (0 or NaN).
+  const float inv = !finite ? __uint_as_float(abits == 0x7F800000u ? 0u : abits)
+                            : e >= -126 ? __uint_as_float((uint32_t)(127 - e) << 23) : 0x1p127f;
+  e8[id] = finite ? (uint8_t)(e + 127) : (uint8_t)255;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     uint32_t w[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int b0 = 16 * i + 4 * k;
-      const float y0 = fminf(fmaxf(f[b0] * inv, -FP8_MAX), FP8_MAX);
-      const float y1 = fminf(fmaxf(f[b0 + 1] * inv, -FP8_MAX), FP8_MAX);
-      const float y2 = fminf(fmaxf(f[b0 + 2] * inv, -FP8_MAX), FP8_MAX);
-      const float y3 = fminf(fmaxf(f[b0 + 3] * inv, -FP8_MAX), FP8_MAX);
-      int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-      pk = __builtin_amdgcn_cvt_pk_fp8_f32(y2, y3, pk, true);
+      int pk = __builtin_amdgcn_cvt_pk_fp8_f32(f[b0] * inv, f[b0 + 1] * inv, 0, false);
+      pk = __builtin_amdgcn_cvt_pk_fp8_f32(f[b0 + 2] * inv, f[b0 + 3] * inv, pk, true);
       w[k] = (uint32_t)pk;
     }
     *(v4i*)(out + 16 * i) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};

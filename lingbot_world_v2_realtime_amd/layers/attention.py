@@ -18,18 +18,22 @@ __all__ = ["attention", "flash_attention", "sage_attention", "CrossAttnCache", "
 
 _QUANT = os.environ.get("LINGBOT_ATTN") in ("sage", "sage_kvq")
 
-# Per-call buffers of the drop-in, kept across calls: (batch, heads, padded keys, device, stream) -> (ring, re-quant
-# workspace). Every block the attention reads is re-quantised by the call itself, so the ring is allocated
-# uninitialised and never cleared; keyed by stream, so calls on different streams never share one.
+# Per-call buffers of the drop-in, kept across calls: (batch, heads, device, stream) -> (ring, re-quant workspace).
+# One ring per key, sized for the most keys a call has asked for so far and reused by every call with fewer (the
+# DiT's key count grows chunk by chunk up to the window, so earlier sizes are never needed again). Every block the
+# attention reads is re-quantised by the call itself, so the ring is allocated uninitialised and never cleared;
+# keyed by stream, so calls on different streams never share one.
 _DROPIN = {}
 
 
 def _dropin_buffers(b, h, lk, device):
-    cap = kernels.pad_to(lk, kernels.K_BLOCK)
     dev = torch.device(device)
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    key = (b, h, cap, idx, torch.cuda.current_stream(idx).cuda_stream)
-    if key not in _DROPIN:
+    key = (b, h, idx, torch.cuda.current_stream(idx).cuda_stream)
+    held = _DROPIN.get(key)
+    if held is None or held[0].cap < lk:
+        cap = kernels.pad_to(lk, kernels.K_BLOCK)
+        _DROPIN.pop(key, None)   # the smaller ring is released before the larger one is taken
         ring = kernels.RingCache(1, b, h, cap, 1, dev, zero=False)
         _DROPIN[key] = (ring, kernels.requant_workspace(1, b * h, cap, dev))
     return _DROPIN[key]
@@ -39,12 +43,14 @@ def sage_attention(q, k, v, tensor_layout="NHD", is_causal=False, sm_scale=None)
     """Quantized attention, the call `sageattn(q, k, v, tensor_layout, is_causal, sm_scale)` makes on sm_120
     (per-warp int8 Q, mean-smoothed per-block int8 K, per-channel fp8 V; lingbot/layers/attention.py:34-35).
 
-    q [B, Lq, H, 128], k/v [B, Lk, H, 128] for "NHD" ([B, H, L, 128] for "HND"), bf16 on the GPU. Returns
-    bf16 in q's layout. The K mean and V scales are taken over all Lk keys (one chunk), so the logits need
-    no per-chunk bias. Raises if liblbw_attn.so is missing: there is no fallback.
+    q [B, Lq, H, 128], k/v [B, Lk, H, 128] for "NHD" ([B, H, L, 128] for "HND"), bf16 (or fp16, rounded to bf16
+    first: the quantisers read bf16) on the GPU. Returns bf16 in q's layout. The K mean and V scales are taken over
+    all Lk keys (one chunk), so the logits need no per-chunk bias. Raises if liblbw_attn.so is missing: there is no
+    fallback.
     """
     if is_causal:
         raise NotImplementedError("the quantized kernel is non-causal; the DiT never calls it causally")
+    q, k, v = (t.to(torch.bfloat16) if t.dtype == torch.float16 else t for t in (q, k, v))
     for name, t in (("q", q), ("k", k), ("v", v)):
         kernels._require_cuda_bf16(name, t)
     b, lq, h, *_ = kernels._dims(q, tensor_layout)
@@ -131,13 +137,15 @@ def cross_attention(q, cache, k_lens=None, softmax_scale=None):
 
 def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=None, q_scale=None,
               causal=False, window_size=(-1, -1), deterministic=False, dtype=None, fa_version=None):
-    """Drop-in for lingbot/layers/attention.py:27-40: same arguments, same routing, q.dtype out."""
+    """Drop-in for lingbot/layers/attention.py:27-40: same arguments, same routing, q.dtype out. Inputs are cast
+    to `dtype` (bf16 by default) as the reference does before its Sage call; an fp16 `dtype` is then rounded to
+    bf16 inside sage_attention. A causal call takes the SDPA route: the quantized kernel is non-causal (the
+    reference hands causal to Sage; the DiT never calls it causally)."""
     dtype = torch.bfloat16 if dtype is None else dtype
     if _QUANT and q_lens is None and k_lens is None and dropout_p == 0. and not causal:
         out_dtype = q.dtype
-        # the kernels quantise from bf16, whatever compute dtype the caller names
-        x = sage_attention(q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16),
-                           tensor_layout="NHD", is_causal=causal, sm_scale=softmax_scale)
+        x = sage_attention(q.to(dtype), k.to(dtype), v.to(dtype), tensor_layout="NHD", is_causal=causal,
+                           sm_scale=softmax_scale)
         return x.to(out_dtype)
     return _paper_attention(q, k, v, q_lens=q_lens, k_lens=k_lens, dropout_p=dropout_p,
                             softmax_scale=softmax_scale, q_scale=q_scale, causal=causal,

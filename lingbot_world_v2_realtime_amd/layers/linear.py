@@ -14,7 +14,8 @@ import torch
 
 from .. import kernels
 
-__all__ = ["FP8Linear", "MXFP8Linear", "convert_to_fp8", "use_tuned_gemms", "tune_gemms", "GEMM_TABLE"]
+__all__ = ["FP8Linear", "MXFP8Linear", "convert_to_fp8", "fp8_eligible", "use_tuned_gemms", "tune_gemms",
+           "GEMM_TABLE"]
 
 # hipBLASLt solutions for the DiT's rowwise FP8 GEMMs at the chunk shape (6032 tokens), as a TunableOp results file:
 # a key per (layout, N, M, K, leading dims, rowwise scales, bias type), the solution, its measured time, and the
@@ -58,7 +59,6 @@ def tune_gemms(shapes, path, device="cuda", bias=True):
 
 class FP8Linear(torch.nn.Module):
     """Rowwise FP8 replacement of an nn.Linear (lingbot/layers/linear.py:10-29)."""
-    FMAX = torch.finfo(torch.float8_e4m3fn).max
 
     def __init__(self, lin):
         super().__init__()
@@ -84,6 +84,7 @@ class FP8Linear(torch.nn.Module):
 
 
 MX_ROWS = 128   # hipBLASLt's MX-scaled GEMM takes row counts in multiples of its 128-row tile
+MX_K = 128      # and K in whole 128-value tiles: four E8M0 scale columns (the reference pads its scales to this too)
 
 
 def _pad(n, m):
@@ -94,17 +95,22 @@ class MXFP8Linear(torch.nn.Module):
     """MXFP8 replacement of an nn.Linear (lingbot/layers/linear.py:53-73): e4m3 with one power-of-two (E8M0)
     scale per 32 values along K for the weights (once) and the activations (every call). The quantisation is
     lbw_quant_mx_fp8; the GEMM is hipBLASLt's MX-scaled FP8 GEMM, whose row counts are padded to 128 (the
-    quantiser writes the padding rows, so nothing is copied), the bias added after it as the reference does."""
+    quantiser writes the padding rows, so nothing is copied), the bias added after it as the reference does.
+    A K that is not a multiple of 128 (the GEMM's scale tile) is padded with zero columns, weights once and
+    activations per call: a zero group quantises to zeros, so the product is unchanged."""
 
     def __init__(self, lin):
         super().__init__()
         w = lin.weight.detach()
         if w.dtype not in (torch.bfloat16, torch.float32):
             w = w.float()
-        n = w.shape[0]
+        n, k = w.shape
+        self.k_pad = _pad(k, MX_K) - k
+        if self.k_pad:
+            w = torch.nn.functional.pad(w, (0, self.k_pad))
         w8, ws = kernels.quant_mx_fp8(w.contiguous(), _pad(n, MX_ROWS))
-        self.register_buffer("w8", w8)             # [Np, K]
-        self.register_buffer("w_scale", ws)        # [Np, K / 32] e8m0
+        self.register_buffer("w8", w8)             # [Np, Kp]
+        self.register_buffer("w_scale", ws)        # [Np, Kp / 32] e8m0
         self.bias = lin.bias
         self.in_features, self.out_features = lin.in_features, lin.out_features
 
@@ -113,6 +119,8 @@ class MXFP8Linear(torch.nn.Module):
         x2 = x.reshape(-1, shape[-1])
         if x2.dtype not in (torch.bfloat16, torch.float32):
             x2 = x2.float()
+        if self.k_pad:
+            x2 = torch.nn.functional.pad(x2, (0, self.k_pad))
         m = x2.shape[0]
         x8, xs = kernels.quant_mx_fp8(x2.contiguous(), _pad(m, MX_ROWS))
         y = torch._scaled_mm(x8, self.w8.t(), scale_a=xs, scale_b=self.w_scale, out_dtype=torch.bfloat16)
@@ -122,18 +130,21 @@ class MXFP8Linear(torch.nn.Module):
         return y.reshape(*shape[:-1], self.out_features)
 
 
+def fp8_eligible(lin, mx=False):
+    """The reference's rule for which linears run in FP8 (lingbot/layers/linear.py:76-89): both dimensions at
+    least 1024, out_features a multiple of 16 and in_features a multiple of 16 (of 32, the scale group, for MX)."""
+    k_mult = 32 if mx else 16
+    return min(lin.in_features, lin.out_features) >= 1024 and lin.out_features % 16 == 0 and \
+        lin.in_features % k_mult == 0
+
+
 def convert_to_fp8(blocks, mx=False):
-    """Swap the large nn.Linear layers inside `blocks` for FP8Linear (or MXFP8Linear), by the reference's rule
-    (lingbot/layers/linear.py:76-89): both features >= 1024, in_features a multiple of 16 (32 for MX),
-    out_features a multiple of 16. Returns (fp8 count, linear count)."""
-    n_all, n_fp8 = 0, 0
-    for parent in list(blocks.modules()):
-        for name, m in list(parent.named_children()):
-            if not isinstance(m, torch.nn.Linear):
-                continue
-            n_all += 1
-            if (m.in_features >= 1024 and m.out_features >= 1024
-                    and m.in_features % (32 if mx else 16) == 0 and m.out_features % 16 == 0):
-                setattr(parent, name, (MXFP8Linear if mx else FP8Linear)(m))
-                n_fp8 += 1
-    return n_fp8, n_all
+    """Replace every eligible nn.Linear below `blocks` (fp8_eligible) by FP8Linear, or MXFP8Linear with mx=True,
+    in place. Returns (replaced, linears seen)."""
+    make = MXFP8Linear if mx else FP8Linear
+    found = [(path, m) for path, m in blocks.named_modules() if path and isinstance(m, torch.nn.Linear)]
+    chosen = [(path, m) for path, m in found if fp8_eligible(m, mx)]
+    for path, m in chosen:
+        owner, _, attr = path.rpartition(".")
+        setattr(blocks.get_submodule(owner), attr, make(m))
+    return len(chosen), len(found)

@@ -1,6 +1,8 @@
 """CPU restatement of the rowwise FP8 quantisation of the FP8 linear layers (test infrastructure only):
 lingbot/layers/linear.py:15-26 -- per row scale = max(amax / 448, 1e-12) in fp32, values x / scale in fp32 cast to
-e4m3 (round to nearest even; |x / scale| <= 448 up to the rounding of the division, which the cast takes to 448)."""
+e4m3 (round to nearest even; |x / scale| <= 448 up to the rounding of the division, which the cast takes to 448).
+Non-finite rows follow torch: a NaN makes the row's scale and every value NaN; an infinity makes the scale inf,
+the row's finite values +-0 and the infinity NaN."""
 import torch
 
 FMAX = 448.0
@@ -26,13 +28,17 @@ def quant_mx(x):
     q is within an ulp above a power of two and its log2 rounds down onto the integer."""
     m, k = x.shape
     xb = x.float().view(m, k // 32, 32)
-    amax = xb.abs().amax(-1).clamp(min=2.0 ** -126)
+    amax = xb.abs().amax(-1).clamp(min=2.0 ** -126)   # NaN if the group holds one (torch's amax propagates it)
     q = amax / torch.tensor(FMAX, dtype=torch.float32)
     f, ex = torch.frexp(q)
     e = torch.where(f == 0.5, ex - 1, ex).clamp(min=-127)
-    scale = torch.ldexp(torch.ones_like(q), e)
+    # a group holding a NaN or an infinity: the reference's scale is NaN / inf (its E8M0 byte 255) and x / scale
+    # is NaN, or +-0 for the finite values of an infinite group
+    finite = torch.isfinite(amax)
+    scale = torch.where(finite, torch.ldexp(torch.ones_like(q), e), amax)
     y = (xb / scale[..., None]).clamp(-FMAX, FMAX)
-    return y.to(torch.float8_e4m3fn).view(torch.uint8).view(m, k), (e + 127).to(torch.uint8)
+    e8 = torch.where(finite, e + 127, torch.full_like(e, 255))
+    return y.to(torch.float8_e4m3fn).view(torch.uint8).view(m, k), e8.to(torch.uint8)
 
 
 def dequant_mx(bits, e8):

@@ -79,6 +79,52 @@ def test_mx_matches_the_reference_formula_away_from_power_of_two_boundaries():
     assert torch.equal(bits, rb)
 
 
+def _nan_equal(a, b):
+    """e4m3 bytes equal, except that any NaN code (0x7F / 0xFF) matches any other: NaN's sign is not defined."""
+    na = (a & 0x7F) == 0x7F
+    nb = (b & 0x7F) == 0x7F
+    return torch.equal(na, nb) and torch.equal(a[~na], b[~nb])
+
+
+def _nonfinite_rows(dtype):
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(4, 128, generator=g)
+    x[0, 5] = float("nan")            # NaN row: everything NaN
+    x[1, 70] = float("inf")           # infinite row: +-0, NaN at the infinity
+    x[1, 3] = -0.0
+    x[2, 0] = -float("inf")
+    return x.to(dtype)
+
+
+def test_rows_nonfinite_follow_the_reference():
+    """A row holding a NaN or an infinity: the reference's formula (amax, clamp, divide, cast; linear.py:15-26) makes
+    the NaN row all NaN, and the infinite rows' finite values signed zeros with NaN at the infinities. The oracle
+    gives the same bytes (up to NaN's sign) and the same scales."""
+    for dtype in (torch.bfloat16, torch.float32):
+        x = _nonfinite_rows(dtype)
+        bits, scale = fp8.quant_rows(x)
+        xf = x.float()
+        rs = (xf.abs().amax(dim=1, keepdim=True) / 448.0).clamp(min=1e-12)
+        rb = (xf / rs).to(torch.float8_e4m3fn).view(torch.uint8)
+        assert _nan_equal(bits, rb)
+        assert torch.isnan(scale[0]).all() and torch.isinf(scale[1:3]).all() and torch.isfinite(scale[3]).all()
+        assert ((bits[0] & 0x7F) == 0x7F).all()
+        assert bits[1, 3] == 0x80 and ((bits[1, 70] & 0x7F) == 0x7F) and ((bits[1] & 0x7F) == 0).sum() == 127
+
+
+def test_mx_nonfinite_groups_follow_the_reference_formula():
+    """Groups holding a NaN or an infinity: the reference's log2 / ceil / exp2 formula gives them a NaN / inf scale,
+    whose E8M0 byte is 255, and x / scale (NaN, or +-0 with NaN at the infinity); finite groups of the same rows keep
+    their normal scales."""
+    x = _nonfinite_rows(torch.bfloat16)
+    bits, e8 = fp8.quant_mx(x)
+    rb, rs = _ref_mx_formula(x)
+    ref_e8 = rs.to(torch.float8_e8m0fnu).view(torch.uint8)
+    assert torch.equal(e8, ref_e8)
+    assert e8[0, 0] == 255 and e8[1, 2] == 255 and e8[2, 0] == 255 and (e8[3] != 255).all()
+    assert _nan_equal(bits, rb)
+
+
 def test_mx_exact_exponent_at_a_boundary():
     """amax / 448 one ulp above 2^k: the exact ceil is k + 1 (so x / scale stays <= 448); fp32 log2 may round
     onto k. A group whose amax / 448 is exactly 2^k gets scale 2^k and its max maps to 448."""

@@ -175,6 +175,59 @@ def test_mxfp8_linear(m, k, n, bias):
     assert e.max().item() <= 1e-2 * ref.abs().max().item()
 
 
+def _nan_equal(a, b):
+    na, nb = (a & 0x7F) == 0x7F, (b & 0x7F) == 0x7F   # any NaN code matches any other (NaN's sign is not defined)
+    return torch.equal(na, nb) and torch.equal(a[~na], b[~nb])
+
+
+def test_quant_nonfinite_rows():
+    """Rows holding a NaN or an infinity, rowwise and MX, against the oracle (which follows the reference's torch
+    formulas): a NaN spreads over its row (its group for MX), an infinity makes the row's (group's) finite values
+    signed zeros and itself NaN, with scale NaN / inf (E8M0 byte 255); the finite rows are untouched."""
+    g = torch.Generator().manual_seed(8)
+    for dtype in (torch.bfloat16, torch.float32):
+        x = torch.randn(6, 1536, generator=g)
+        x[1, 700] = float("nan")
+        x[2, 3] = float("inf")
+        x[2, 4] = -0.0
+        x[4, 1535] = -float("inf")
+        x = x.to(dtype)
+        x8, sc = _k().quant_rows_fp8(x.to(DEV))
+        m8, me = _k().quant_mx_fp8(x.to(DEV), 128)
+        torch.cuda.synchronize()
+        rb, rs = fp8.quant_rows(x)
+        assert _nan_equal(x8.view(torch.uint8).cpu(), rb)
+        assert torch.equal(sc.cpu().isnan(), rs.isnan()) and torch.equal(sc.cpu()[~rs.isnan()], rs[~rs.isnan()])
+        mb, mer = fp8.quant_mx(x)
+        assert _nan_equal(m8.view(torch.uint8)[:6].cpu(), mb)
+        assert torch.equal(me.view(torch.uint8)[:6].cpu(), mer)
+        assert int(x8.view(torch.uint8)[2, 4].cpu()) == 0x80 and (mer[2, 0] == 255) and (mer[2, 1:] != 255).all()
+
+
+def test_mxfp8_linear_k_not_a_multiple_of_128():
+    """in_features 1056 (33 scale groups): the weights and activations are padded with zero columns to 1152 for
+    the GEMM's 128-wide scale tile, which leaves the product unchanged: against fp32 of the unpadded MX operands."""
+    from lingbot_world_v2_realtime_amd.layers.linear import MXFP8Linear
+    g = torch.Generator().manual_seed(9)
+    m, k, n = 100, 1056, 1536
+    lin = torch.nn.Linear(k, n, bias=True).to(torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(n, k, generator=g) * 0.02)
+        lin.bias.copy_(torch.randn(n, generator=g) * 0.1)
+    f = MXFP8Linear(lin.to(DEV))
+    assert f.w8.shape == (1536, 1152) and f.k_pad == 96
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    y = f(x.to(DEV))
+    torch.cuda.synchronize()
+    xb, xe = fp8.quant_mx(x)
+    wb, we = fp8.quant_mx(lin.weight.detach().cpu())
+    ref = fp8.dequant_mx(xb, xe) @ fp8.dequant_mx(wb, we).t() + lin.bias.detach().cpu().float()
+    e = (y.float().cpu() - ref).abs()
+    record(f"MXFP8Linear {m}x{k}x{n} (K padded to 1152): vs same-operand fp32 max {e.max().item():.2e} "
+           f"(|ref| max {ref.abs().max().item():.2e})")
+    assert e.max().item() <= 1e-2 * ref.abs().max().item()
+
+
 def test_convert_to_fp8_mx_selection():
     from lingbot_world_v2_realtime_amd.layers.linear import MXFP8Linear, convert_to_fp8
     blk = torch.nn.Sequential(torch.nn.Linear(1536, 1536), torch.nn.Linear(1040, 1536)).to(torch.bfloat16).to(DEV)

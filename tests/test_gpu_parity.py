@@ -446,6 +446,36 @@ def test_sage_kvq_surface():
     assert set(cache) == {"k", "v"}
 
 
+def test_dropin_keeps_one_ring_per_stream():
+    """The drop-in keeps one quantised ring per (batch, heads, device, stream), grown to the most keys asked for and
+    reused by calls with fewer: 300, 700, then 300 keys leave one 704-token ring, and the repeated call is
+    bit-identical to the first."""
+    from lingbot_world_v2_realtime_amd import sage_attention
+    from lingbot_world_v2_realtime_amd.layers import attention as attn_mod
+    h = 5
+    q, k, v, _ = emu.make_inputs(200, 700, h=h, seed=73)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    a1 = sage_attention(q, k[:, :300], v[:, :300])
+    a2 = sage_attention(q, k, v)
+    a3 = sage_attention(q, k[:, :300], v[:, :300])
+    torch.cuda.synchronize()
+    held = [val for key, val in attn_mod._DROPIN.items() if key[:2] == (1, h)]
+    assert len(held) == 1 and held[0][0].cap == 704
+    assert torch.equal(a1, a3) and not torch.equal(a1, a2)
+
+
+def test_dropin_fp16_inputs_round_to_bf16():
+    """fp16 inputs (what attention(..., dtype=torch.float16) hands over) are rounded to bf16 before quantisation:
+    the same bits as the call on the bf16-rounded tensors."""
+    from lingbot_world_v2_realtime_amd import sage_attention
+    q, k, v, _ = emu.make_inputs(300, 500, h=2, seed=74)
+    qh, kh, vh = (x.float().half().to(DEV) for x in (q, k, v))
+    got = sage_attention(qh, kh, vh)
+    want = sage_attention(*(x.to(torch.bfloat16) for x in (qh, kh, vh)))
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16 and torch.equal(got, want)
+
+
 def test_hnd_layout_same_bits():
     """tensor_layout="HND" ([B, H, L, 128]) reads the same elements through other strides: the output is the
     NHD call's, bit for bit, with a custom sm_scale, and it is close to fp32 SDPA."""

@@ -118,6 +118,19 @@ def test_attention_routing(monkeypatch):
     assert len(calls) == 1
 
 
+def test_attention_casts_to_dtype(monkeypatch):
+    """As the reference does (lingbot/layers/attention.py:30-35), the quantized route gets q / k / v cast to
+    `dtype` (bf16 when None) and the result comes back in q's dtype."""
+    seen = []
+    monkeypatch.setattr(attn_mod, "_QUANT", True)
+    monkeypatch.setattr(attn_mod, "sage_attention", lambda q, k, v, **kw: seen.append((q.dtype, k.dtype, v.dtype))
+                        or q.clone())
+    q = torch.randn(1, 16, 2, 128)
+    assert attn_mod.attention(q, q, q).dtype == torch.float32
+    assert attn_mod.attention(q, q, q, dtype=torch.float16).dtype == torch.float32
+    assert seen == [(torch.bfloat16,) * 3, (torch.float16,) * 3]
+
+
 class _no_warn:
     def __enter__(self):
         return self
