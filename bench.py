@@ -76,24 +76,35 @@ def requant_bytes(n, h=H, d=D, v_planes=1):
     return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + 2 * h * d * 4
 
 
-def traffic_from_profiles():
-    """HBM bytes of one attention call (attn_fwd_kernel + merge) measured with rocprofv3 --pmc (FETCH_SIZE and
-    WRITE_SIZE, scaled by a copy of known size), as committed in profiles/; None when not measured."""
-    p = os.path.join(ROOT, "profiles", "attn_fwd_cfg3_traffic.json")
-    if not os.path.exists(p):
-        return None
-    with open(p) as f:
-        return json.load(f).get("call_hbm_bytes")
-
-
-def counters_from_profiles():
-    """MFMA counters of the attention kernel (rocprofv3 --pmc: SQ_INSTS_VALU_MFMA_MOPS_I8 / _F8 and
-    SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE), as committed in profiles/; None when not measured."""
-    p = os.path.join(ROOT, "profiles", "attn_fwd_cfg3_counters.json")
+def _profile(name):
+    """A counter summary committed in profiles/ (None when absent), with the source fingerprint of the build it
+    was measured on (`sources_sha16`, lingbot_world_v2_realtime_amd._lib.sources_sha16)."""
+    p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
         return None
     with open(p) as f:
         return json.load(f)
+
+
+def traffic_from_profiles(build):
+    """HBM bytes of one attention call (attn_fwd_kernel + merge) measured with rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE, scaled by a copy of known size), as committed in profiles/: (bytes, the fingerprint of the build
+    they were measured on). The bytes are None unless that build is `build`, the one this run loaded."""
+    prof = _profile("attn_fwd_cfg3_traffic.json")
+    if prof is None:
+        return None, None
+    sha = prof.get("sources_sha16")
+    return (prof.get("call_hbm_bytes") if sha == build else None), sha
+
+
+def counters_from_profiles(build):
+    """MFMA counters of the attention kernel (rocprofv3 --pmc: SQ_INSTS_VALU_MFMA_MOPS_I8 / _F8 and
+    SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE), as committed in profiles/, with the fingerprint of the build
+    they were measured on; None unless that build is `build`."""
+    prof = _profile("attn_fwd_cfg3_counters.json")
+    if prof is None or prof.get("sources_sha16") != build:
+        return None
+    return prof
 
 
 def cpu_baseline(heads=3, q_rows=LQ):
@@ -195,10 +206,10 @@ def profile_only(args, dev):
             mk = torch.randn(1, CHUNK, H, D, device=dev).to(torch.bfloat16)
             ring.write(0, mk, mk)
             ring.commit()
-        print(json.dumps({"only": "prologue", "result": prologue_call(dev, ring, args.steps)}), flush=True)
+        print(json.dumps({"only": "prologue", "result": prologue_call(dev, ring, args.steps, args.warmup)}), flush=True)
         return
     elif args.only == "cross":
-        print(json.dumps({"only": "cross", "result": cross_attention_call(dev, args.steps)}), flush=True)
+        print(json.dumps({"only": "cross", "result": cross_attention_call(dev, args.steps, args.warmup)}), flush=True)
         return
     elif args.only == "requant":
         kl = torch.randn(LAYERS, 1, CHUNK, H, D, device=dev).to(torch.bfloat16)
@@ -281,7 +292,7 @@ def prologue_bytes(n=CHUNK, h=H, d=D, n_seg=MEM + 1):
     return 3 * n * h * d * 2 + 3 * n * h * d + h * (lp // 32) * 4 + n_seg * h * lp * 4 + nb * h * 4 + 2 * h * d * 4
 
 
-def prologue_call(dev, ring, steps=50):
+def prologue_call(dev, ring, steps=50, warmup=5):
     """The self-attention prologue fused into the quantisation, per layer call at the chunk shape: RMSNorm +
     RoPE of the q projection into int8 Q (+ the 4-chunk logit bias), and of the k projection into the roped K
     and the current chunk's ring slot (lbw_norm_rope_quant_q + lbw_norm_rope_kv_requant), on `ring`'s layer 0."""
@@ -304,7 +315,7 @@ def prologue_call(dev, ring, steps=50):
     def qpart():
         kernels.norm_rope_quant_q(ql, H, wq, 1e-6, rope, ring.cache, 0, slots)
 
-    for _ in range(5):
+    for _ in range(warmup):
         kpart(), qpart()
     torch.cuda.synchronize()
     k_ms = _timed(kpart, steps, stream)
@@ -319,7 +330,7 @@ BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 CONTEXT = 512               # text context tokens of the cross-attention
 
 
-def cross_attention_call(dev, steps=50):
+def cross_attention_call(dev, steps=50, warmup=5):
     """The DiT's cross-attention per layer call: Q [1,6032,12,128] bf16 against the 512-token text context
     (prepared once per generation), bf16 flash attention on the MFMA with fp32 accumulation (lbw_cross_attn_fwd).
     Algorithmic flops 4 * H * Lq * Lk * d against the dense bf16 peak."""
@@ -330,7 +341,7 @@ def cross_attention_call(dev, steps=50):
     k, v = (torch.randn(1, CONTEXT, H, D, device=dev, generator=g).to(torch.bfloat16) for _ in range(2))
     ctx = kernels.CrossContext(k, v)
     out = torch.empty_like(q)
-    for _ in range(5):
+    for _ in range(warmup):
         kernels.cross_attn_fwd(q, ctx, out)
     torch.cuda.synchronize()
     ms = _timed(lambda: kernels.cross_attn_fwd(q, ctx, out), steps, torch.cuda.current_stream(dev))
@@ -433,9 +444,10 @@ def main():
         sys.exit(2)
 
     import torch
-    from lingbot_world_v2_realtime_amd import kernels
+    from lingbot_world_v2_realtime_amd import _lib, kernels
     from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
 
+    build = _lib.sources_sha16()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if args.only:
@@ -523,21 +535,28 @@ def main():
                    "head_dim": D},
         "roofline": {"bound": "mfma", "achieved": round(attn_tops, 2), "peak": MFMA_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(attn_tops / MFMA_PEAK_TOPS, 4),
-                     "traffic": traffic_from_profiles(),
+                     "traffic": None,
                      "kernel": "lbw_attn_fwd = attn_fwd_kernel + attn_merge_kernel", "kernel_ms": round(attn_ms, 4),
-                     "ops_per_launch": ops},
+                     "ops_per_launch": ops, "build_sha16": build},
         "requant": {"layers": LAYERS, "ms": round(rq_ms, 4), "algorithmic_bytes": rq_bytes,
                     "GB/s": round(rq_gbps, 1), "frac_hbm": round(rq_gbps / HBM_PEAK_GBPS, 4),
                     "bytes_moved_two_v_planes": rq_moved},
     }
-    ctr = counters_from_profiles()
+    # traffic and counters come from rocprofv3 runs committed in profiles/; they count only when those runs
+    # measured this very build (same source fingerprint), and the line says which build they are from
+    traffic, traffic_build = traffic_from_profiles(build)
+    res["roofline"]["traffic"] = traffic
+    res["roofline"]["traffic_source"] = {"file": "profiles/attn_fwd_cfg3_traffic.json", "build_sha16": traffic_build,
+                                         "matches_this_build": traffic_build == build}
+    ctr = counters_from_profiles(build)
     if ctr is not None:   # issued MFMA work from the counters, over this run's HIP-event time
         issued = ctr["issued_ops"]
         res["roofline"]["counters"] = {
             "issued_ops_per_launch": issued, "issued_over_algorithmic": round(issued / ops, 4),
             "issued_TOPS": round(issued / (attn_ms * 1e-3) / 1e12, 1),
             "issued_frac": round(issued / (attn_ms * 1e-3) / 1e12 / MFMA_PEAK_TOPS, 4),
-            "mfma_busy": round(ctr["mfma_busy"], 4), "source": "profiles/attn_fwd_cfg3_counters.json"}
+            "mfma_busy": round(ctr["mfma_busy"], 4), "profiled_kernel_ms": ctr.get("kernel_ms"),
+            "source": "profiles/attn_fwd_cfg3_counters.json", "build_sha16": ctr["sources_sha16"]}
     res["prologue"] = prologue_call(dev, ring)
     res["cross_attention"] = cross_attention_call(dev)
     res["fp8_linear"] = fp8_linear_calls(dev)

@@ -37,6 +37,23 @@ SIGNATURES = {
 }
 
 
+def sources_sha16():
+    """First 16 hex digits of a sha256 over what liblbw_attn.so is built from: the HIP sources and headers (csrc/,
+    include/) and the compiler flags. A measurement stored with this fingerprint describes this build when the
+    fingerprints match."""
+    import hashlib
+    from . import build
+    here = os.path.dirname(os.path.abspath(__file__))
+    files = [os.path.join(here, "csrc", f) for f in sorted(os.listdir(os.path.join(here, "csrc")))
+             if f.endswith((".hip", ".h"))]
+    files.append(os.path.join(os.path.dirname(here), "include", "lbw_attn.h"))
+    h = hashlib.sha256(" ".join(build.HIPCC_FLAGS).encode())
+    for f in files:
+        with open(f, "rb") as fh:
+            h.update(os.path.basename(f).encode() + b"\0" + fh.read())
+    return h.hexdigest()[:16]
+
+
 class LbwError(RuntimeError):
     pass
 
