@@ -20,6 +20,8 @@ Reported (one JSON line on stdout):
                flops / time, vs 5.0 PFLOP/s dense fp8
   chunk_sweep  the whole chunk captured in one HIP graph: 30 layers x 5 passes of the step above, then the
                30-layer re-quant that saves the chunk; seconds per chunk
+  chunk_sweep_fused  the same chunk as the DiT block runs it from its q / k / v projections: 30 layers x 5
+               passes of the fused prologue + attention (causal_self_attention), one HIP graph
   cpu_baseline the torch CPU emulation of the same scheme (oracle/emu.py) on a bounded sample of the call
 """
 import argparse
@@ -281,6 +283,54 @@ def chunk_sweep(dev, layers=LAYERS, passes=5, replays=3):
     calls = passes * layers
     return {"calls": calls, "layers": layers, "passes": passes, "s_per_chunk": round(sec, 5),
             "attention_TOPS": round(calls * attention_ops(LQ, LK) / sec / 1e12, 1), "hip_graph": True}
+
+
+def chunk_sweep_fused(dev, layers=LAYERS, passes=5, replays=3):
+    """The whole chunk as a DiT block runs it from its projections: `passes` forwards of `layers` layers, each
+    layer call the fused self-attention (causal_self_attention: RMSNorm + RoPE of the q / k projections into the
+    int8 Q and the current chunk's ring slot, then attention over the chunk + 3 cached chunks, 24128 keys).
+    Every forward re-quantises the current slot, so the last (clean) pass is the save and no separate 30-layer
+    re-quant follows. Captured once in a HIP graph and replayed; seconds per chunk and attention TOPS."""
+    import torch
+    from lingbot_world_v2_realtime_amd.layers.kv_quant import QuantKVRing
+    from lingbot_world_v2_realtime_amd.layers.prologue import ChunkRope, causal_self_attention, rope_freqs
+    g = torch.Generator(device=dev).manual_seed(7)
+    ql, kl = (torch.randn(1, CHUNK, H * D, device=dev, generator=g).to(torch.bfloat16) for _ in range(2))
+    v = torch.randn(1, CHUNK, H, D, device=dev, generator=g).to(torch.bfloat16)
+    wq, wk = ((1 + 0.3 * torch.randn(H * D, device=dev, generator=g)).to(torch.bfloat16) for _ in range(2))
+    rope = ChunkRope.for_chunk(rope_freqs(dev), (4, 29, 52), current_start=MEM * CHUNK)
+    ring = QuantKVRing(layers, 1, H, CHUNK, slots=MEM + 1, device=dev)
+    mk = torch.randn(layers, 1, CHUNK, H, D, device=dev, generator=g).to(torch.bfloat16)
+    for _ in range(MEM):
+        ring.write_layers(mk, mk)
+        ring.commit()
+    del mk
+    k_out = torch.empty(1, CHUNK, H, D, device=dev, dtype=torch.bfloat16)
+
+    def chunk():
+        for _ in range(passes):
+            for layer in range(layers):
+                causal_self_attention(ring, layer, ql, kl, v, H, wq, wk, rope, k_out=k_out)
+
+    chunk()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        chunk()
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / replays
+    calls = passes * layers
+    return {"calls": calls, "layers": layers, "passes": passes, "s_per_chunk": round(sec, 5),
+            "attention_TOPS": round(calls * attention_ops(LQ, LK) / sec / 1e12, 1), "hip_graph": True,
+            "per_call": "norm_rope_quant_q + norm_rope_kv_requant (stats, finalise, quant) + attention"}
 
 
 def prologue_bytes(n=CHUNK, h=H, d=D, n_seg=MEM + 1):
@@ -562,6 +612,7 @@ def main():
     res["fp8_linear"] = fp8_linear_calls(dev)
     res["dropin_call"] = dropin_call(dev)
     res["chunk_sweep"] = None if args.no_sweep else chunk_sweep(dev)
+    res["chunk_sweep_fused"] = None if args.no_sweep else chunk_sweep_fused(dev)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_heads)
     else:

@@ -54,6 +54,10 @@ enum {
 #define LBW_HEAD_DIM 128
 #define LBW_MAX_SEGMENTS 8
 
+/* The 16-bit input formats of lbw_kv_requant and lbw_quant_q (their `dtype` argument). */
+#define LBW_DTYPE_BF16 0
+#define LBW_DTYPE_FP16 1
+
 /* Name of a status code. */
 const char* lbw_status_string(int status);
 
@@ -64,16 +68,17 @@ int lbw_version(void);
 int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len);
 
 /*
- * Quantise bf16 K and V chunks of `len` tokens into slot `slot` of `layers` consecutive layer caches:
- * the per-(head, channel) K mean, K - mean as int8 per 64-token block, V as e4m3 with one scale per
- * (head, channel), plus the residual plane when v8lo is not null. Replaces sage_kvq.requant_all + write_chunk (experiments/modules/sage_kvq.py:78-98)
+ * Quantise K and V chunks of `len` tokens (bf16, or fp16 with dtype LBW_DTYPE_FP16: 16-bit words either way) into
+ * slot `slot` of `layers` consecutive layer caches: the per-(head, channel) K mean (rounded to the inputs' own
+ * format, as the reference's k.mean of such a tensor), K - mean as int8 per 64-token block, V as e4m3 with one scale
+ * per (head, channel), plus the residual plane when v8lo is not null. Replaces sage_kvq.requant_all + write_chunk (experiments/modules/sage_kvq.py:78-98)
  * and Sage's per_warp_int8 K part / per_channel_fp8 (lingbot/layers/sage_preq.py:115-124).
  * k/v element (layer l, batch b, token t, head h, channel d) sits at l*s_layer + b*s_batch + t*s_tok
  * + h*s_head + d. `workspace` holds lbw_kv_requant_workspace_bytes() bytes, 16-byte aligned; its
  * contents need not be preserved between calls, and calls that share a workspace must not overlap. Tokens in [len, ceil64(len)) of the slot are written
  * as zero; blocks past ceil64(len) are left untouched (the attention never reads them).
  */
-int lbw_kv_requant(const uint16_t* k, const uint16_t* v,
+int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int dtype,
                    int64_t layers, int64_t batch, int64_t len, int64_t heads,
                    int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok, int64_t k_s_head,
                    int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
@@ -82,13 +87,14 @@ int lbw_kv_requant(const uint16_t* k, const uint16_t* v,
                    void* workspace, void* stream);
 
 /*
- * Quantise bf16 Q [batch][lq][heads][128] (strides s_batch, s_tok, s_head) to int8 with one scale per
+ * Quantise Q [batch][lq][heads][128] (bf16, or fp16 with dtype LBW_DTYPE_FP16; strides s_batch, s_tok, s_head) to
+ * int8 with one scale per
  * 32 rows (Sage per_warp_int8 Q part with BLKQ=128, WARPQ=32: lingbot/layers/sage_preq.py:116,
  * experiments/modules/sage_kvq.py:104). When n_seg > 1 it also writes bias[c][bh][row] = q . km of chunk
  * seg_slot[c] of the (layer-offset) cache `km` with `slots` slots; km is then 16-byte aligned. seg_slot is a
  * host array.
  */
-int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads,
+int lbw_quant_q(const uint16_t* q, int dtype, int64_t batch, int64_t lq, int64_t heads,
                 int64_t s_batch, int64_t s_tok, int64_t s_head,
                 int8_t* q8, float* q_scale,
                 const float* km, int64_t slots, int n_seg, const int32_t* seg_slot, float* bias,

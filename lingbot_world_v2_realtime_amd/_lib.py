@@ -11,10 +11,10 @@ SIGNATURES = {
     "lbw_status_string": (ctypes.c_char_p, [_i32]),
     "lbw_version": (_i32, []),
     "lbw_kv_requant_workspace_bytes": (_i64, [_i64, _i64, _i64]),
-    "lbw_kv_requant": (_i32, [_p, _p, _i64, _i64, _i64, _i64,
+    "lbw_kv_requant": (_i32, [_p, _p, _i32, _i64, _i64, _i64, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p]),
-    "lbw_quant_q": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p]),
+    "lbw_quant_q": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i32, _p, _p, _p]),
     "lbw_norm_rope_quant_q": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _p, _f32, _p, _i64, _i64, _i64, _i64,
                                      _p, _p, _p, _i64, _i32, _p, _p, _p, _i64, _i64, _i64, _p]),
     "lbw_norm_rope_kv_requant": (_i32, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _f32,

@@ -28,7 +28,9 @@ struct ReqArgs {
 constexpr int REQ_SUPER = 4;   // blocks per super-block of the mean's defined order
 constexpr int FIN_U = 8;       // super-block sums per lane the finaliser holds in LDS at a time
 
-// Thread (cg, q) = (t & 15, t >> 4) sums channels 8 cg .. + 8 over tokens 4 q .. 4 q + 3 of the block.
+// Thread (cg, q) = (t & 15, t >> 4) sums channels 8 cg .. + 8 over tokens 4 q .. 4 q + 3 of the block. F16: the
+// inputs are fp16 (else bf16).
+template <bool F16>
 __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, ReqArgs a,
                                                        float* __restrict__ part_sum,
@@ -54,8 +56,8 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float kf[8], vf[8];
-    unpack8(kw[j], kf);
-    unpack8(vw[j], vf);
+    unpack8t<F16>(kw[j], kf);
+    unpack8t<F16>(vw[j], vf);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       s[c] = __fadd_rn(s[c], kf[c]);
@@ -87,6 +89,7 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
 // once, in parallel), and the maxima; then one thread per channel sums the U left to right.
 constexpr int FIN_CH = 16;                 // channels per finaliser workgroup
 constexpr int FIN_J = 256 / FIN_CH;        // super-block lanes per channel
+template <bool F16>
 __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float* __restrict__ part_sum,
                                                           const float* __restrict__ part_amax,
                                                           float* __restrict__ v_recip, float* __restrict__ km,
@@ -126,7 +129,7 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
     for (int jj = 1; jj < FIN_J; ++jj) mx = fmaxf(mx, s_mx[jj][c]);
     mx = fmaxf(mx, AMAX_FLOOR);
     const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + ch;
-    km[so] = bf16_round(__fdiv_rn(tot, (float)a.len));
+    km[so] = round16<F16>(__fdiv_rn(tot, (float)a.len));   // the mean in the inputs' own format
     // amax = f * 2^x with f in [0.5, 1) (mx is a normal float): 2^e takes it into (224, 448] = (0.875 * 2^8,
     // 0.875 * 2^9] with e = x - 9 when f <= 0.875 (mantissa bits <= 0x600000), else x - 8; x = biased exponent - 126
     const uint32_t mb = __float_as_uint(mx);
@@ -140,6 +143,7 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
 // e4m3 V bytes for one channel are 4 adjacent positions (one dword) of the permuted layout. Layers go last to
 // first: the statistics pass read the last layers most recently, so the first re-reads can still find them in
 // the memory-side cache.
+template <bool F16>
 __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, ReqArgs a,
                                                        const float* __restrict__ v_recip,
@@ -173,8 +177,8 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
     v4i kw = ok ? *(const v4i*)(kp + tok * a.k_st) : v4i{0, 0, 0, 0};
     v4i vw = ok ? *(const v4i*)(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
     float kf[8], vf[8];
-    unpack8(kw, kf);
-    unpack8(vw, vf);
+    unpack8t<F16>(kw, kf);
+    unpack8t<F16>(vw, vf);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       x[j][c] = ok ? __fsub_rn(kf[c], mean[c]) : 0.f;
@@ -245,7 +249,7 @@ int kv_requant_check(int64_t layers, int64_t batch, int64_t len, int64_t heads, 
   return LBW_OK;
 }
 
-int kv_requant_launch(bool with_stats, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
+int kv_requant_launch(bool with_stats, bool f16, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
                       int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok,
                       int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
                       int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,
@@ -270,10 +274,18 @@ int kv_requant_launch(bool with_stats, const uint16_t* k, const uint16_t* v, int
   if (const int dv = check_device()) return dv;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
-  if (with_stats) hipLaunchKernelGGL(kv_stats_kernel, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
-  hipLaunchKernelGGL(kv_finalize_kernel, dim3((unsigned)a.bh, (unsigned)layers, D / FIN_CH), dim3(256), 0, st, a,
-                     part_sum, part_amax, v_recip, km, v_scale);
-  hipLaunchKernelGGL(kv_quant_kernel, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
+  const dim3 fgrid((unsigned)a.bh, (unsigned)layers, D / FIN_CH);
+  if (f16) {
+    if (with_stats) hipLaunchKernelGGL(kv_stats_kernel<true>, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
+    hipLaunchKernelGGL(kv_finalize_kernel<true>, fgrid, dim3(256), 0, st, a, part_sum, part_amax, v_recip, km,
+                       v_scale);
+    hipLaunchKernelGGL(kv_quant_kernel<true>, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
+  } else {
+    if (with_stats) hipLaunchKernelGGL(kv_stats_kernel<false>, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
+    hipLaunchKernelGGL(kv_finalize_kernel<false>, fgrid, dim3(256), 0, st, a, part_sum, part_amax, v_recip, km,
+                       v_scale);
+    hipLaunchKernelGGL(kv_quant_kernel<false>, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
+  }
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }
@@ -288,13 +300,15 @@ extern "C" int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, in
   return (4 * layers * bh * nb * D + layers * bh * D) * (int64_t)sizeof(float);
 }
 
-extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
+extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int dtype, int64_t layers, int64_t batch,
                               int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch,
                               int64_t k_s_tok, int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch,
                               int64_t v_s_tok, int64_t v_s_head, int8_t* k8, float* k_scale, float* km,
                               uint8_t* v8, uint8_t* v8lo, float* v_scale, int64_t slots, int64_t cap,
                               int64_t slot, void* workspace, void* stream) {
-  return kv_requant_launch(true, k, v, layers, batch, len, heads, k_s_layer, k_s_batch, k_s_tok, k_s_head,
+  if (dtype != LBW_DTYPE_BF16 && dtype != LBW_DTYPE_FP16) return LBW_E_SHAPE;
+  return kv_requant_launch(true, dtype == LBW_DTYPE_FP16, k, v, layers, batch, len, heads, k_s_layer, k_s_batch,
+                           k_s_tok, k_s_head,
                            v_s_layer, v_s_batch, v_s_tok, v_s_head, k8, k_scale, km, v8, v8lo, v_scale, slots,
                            cap, slot, workspace, stream);
 }

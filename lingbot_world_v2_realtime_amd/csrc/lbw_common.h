@@ -1,6 +1,7 @@
 // Shared device helpers of the gfx950 quantized attention kernels.
 #pragma once
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <climits>
@@ -64,6 +65,32 @@ __device__ __forceinline__ void unpack8(const v4i w, float* f) {
     f[2 * i] = __uint_as_float(u << 16);
     f[2 * i + 1] = __uint_as_float(u & 0xFFFF0000u);
   }
+}
+
+// The 16-bit input formats of the quantisers: bf16, or IEEE fp16 (LBW_DTYPE_FP16).
+template <bool F16>
+__device__ __forceinline__ float lo16(uint32_t u) {   // the low 16-bit value of a word, exactly, as fp32
+  if constexpr (F16) return __half2float(__ushort_as_half((unsigned short)(u & 0xFFFFu)));
+  else return __uint_as_float(u << 16);
+}
+template <bool F16>
+__device__ __forceinline__ float hi16(uint32_t u) {   // the high one
+  if constexpr (F16) return __half2float(__ushort_as_half((unsigned short)(u >> 16)));
+  else return __uint_as_float(u & 0xFFFF0000u);
+}
+template <bool F16>
+__device__ __forceinline__ void unpack8t(const v4i w, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = lo16<F16>((uint32_t)w[i]);
+    f[2 * i + 1] = hi16<F16>((uint32_t)w[i]);
+  }
+}
+// fp32 -> the nearest value of the 16-bit format (ties to even), as fp32; finite inputs
+template <bool F16>
+__device__ __forceinline__ float round16(float x) {
+  if constexpr (F16) return __half2float(__float2half_rn(x));
+  else return bf16_round(x);
 }
 
 // round(x * recip) to int8 with saturation; explicit roundings so no FMA contraction can occur.
@@ -135,7 +162,7 @@ int check_device();
 int kv_requant_check(int64_t layers, int64_t batch, int64_t len, int64_t heads, const int8_t* k8,
                      const float* k_scale, const float* km, const uint8_t* v8, const uint8_t* v8lo,
                      const float* v_scale, int64_t slots, int64_t cap, int64_t slot);
-int kv_requant_launch(bool with_stats, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
+int kv_requant_launch(bool with_stats, bool f16, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
                       int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok,
                       int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
                       int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,

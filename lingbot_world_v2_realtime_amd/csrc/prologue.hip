@@ -431,7 +431,7 @@ extern "C" int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, in
     hipLaunchKernelGGL(norm_rope_k_kernel<1024>, grid, block, 0, (hipStream_t)stream, k, v, norm_weight,
                        (const double2*)rope, a, k_out, part_sum, part_amax);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
-  return kv_requant_launch(false, k_out, v, 1, batch, len, heads, 0, o_s_batch, o_s_tok, o_s_head, 0, v_s_batch,
+  return kv_requant_launch(false, false, k_out, v, 1, batch, len, heads, 0, o_s_batch, o_s_tok, o_s_head, 0, v_s_batch,
                            v_s_tok, v_s_head, k8, k_scale, km, v8, v8lo, v_scale, slots, cap, slot, workspace,
                            stream);
 }

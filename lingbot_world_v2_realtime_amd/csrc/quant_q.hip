@@ -15,7 +15,9 @@ struct QArgs {
 // (lane >> 4, lane & 15) holds channels 8 g .. 8 g + 7 of rows 4 (rq + 4 s) + j, s = 0, 1, j = 0..3, so each
 // 16-byte load instruction reads 4 rows x 256 contiguous bytes. The logit bias of a row is its 16 lanes' 8-term
 // dot products with the chunk mean, summed pairwise (xor 1, 2, 4, 8).
+// F16: q is fp16 (else bf16).
 constexpr int QQ_WAVES = 4;
+template <bool F16>
 __global__ __launch_bounds__(64 * QQ_WAVES) void quant_q_kernel(const uint16_t* __restrict__ q, QArgs a,
                                                                int8_t* __restrict__ q8, float* __restrict__ q_scale,
                                                                const float* __restrict__ km,
@@ -44,8 +46,7 @@ __global__ __launch_bounds__(64 * QQ_WAVES) void quant_q_kernel(const uint16_t* 
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(x[s][j][c] << 16)),
-                                 fabsf(__uint_as_float(x[s][j][c] & 0xFFFF0000u))));
+        amax = fmaxf(amax, fmaxf(fabsf(lo16<F16>(x[s][j][c])), fabsf(hi16<F16>(x[s][j][c]))));
   amax = fmaxf(wave_max(amax), AMAX_FLOOR);
   const float recip = __fdiv_rn(127.f, amax);
   if (lane == 0) q_scale[bh * (a.lp / QG) + grp] = __fdiv_rn(amax, 127.f);
@@ -58,10 +59,10 @@ __global__ __launch_bounds__(64 * QQ_WAVES) void quant_q_kernel(const uint16_t* 
 #pragma unroll
       for (int hw = 0; hw < 2; ++hw) {
         const uint32_t u0 = x[s][j][2 * hw], u1 = x[s][j][2 * hw + 1];
-        wd[hw] = ((uint32_t)quant_i8(__uint_as_float(u0 << 16), recip) & 0xFFu) |
-                 (((uint32_t)quant_i8(__uint_as_float(u0 & 0xFFFF0000u), recip) & 0xFFu) << 8) |
-                 (((uint32_t)quant_i8(__uint_as_float(u1 << 16), recip) & 0xFFu) << 16) |
-                 (((uint32_t)quant_i8(__uint_as_float(u1 & 0xFFFF0000u), recip) & 0xFFu) << 24);
+        wd[hw] = ((uint32_t)quant_i8(lo16<F16>(u0), recip) & 0xFFu) |
+                 (((uint32_t)quant_i8(hi16<F16>(u0), recip) & 0xFFu) << 8) |
+                 (((uint32_t)quant_i8(lo16<F16>(u1), recip) & 0xFFu) << 16) |
+                 (((uint32_t)quant_i8(hi16<F16>(u1), recip) & 0xFFu) << 24);
       }
       *(uint2*)(q8 + (bh * a.lp + t) * D + g * 8) = make_uint2(wd[0], wd[1]);
     }
@@ -76,8 +77,8 @@ __global__ __launch_bounds__(64 * QQ_WAVES) void quant_q_kernel(const uint16_t* 
         float acc = 0.f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          acc = fmaf(__uint_as_float(x[s][j][e] << 16), mv[2 * e], acc);
-          acc = fmaf(__uint_as_float(x[s][j][e] & 0xFFFF0000u), mv[2 * e + 1], acc);
+          acc = fmaf(lo16<F16>(x[s][j][e]), mv[2 * e], acc);
+          acc = fmaf(hi16<F16>(x[s][j][e]), mv[2 * e + 1], acc);
         }
         acc = row16_sum(acc);
         if (g == 0) bias[((int64_t)c * a.bh + bh) * a.lp + row0 + 4 * (rq + 4 * s) + j] = acc;
@@ -89,10 +90,11 @@ __global__ __launch_bounds__(64 * QQ_WAVES) void quant_q_kernel(const uint16_t* 
 
 using namespace lbw;
 
-extern "C" int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t heads, int64_t s_batch,
+extern "C" int lbw_quant_q(const uint16_t* q, int dtype, int64_t batch, int64_t lq, int64_t heads, int64_t s_batch,
                            int64_t s_tok, int64_t s_head, int8_t* q8, float* q_scale, const float* km,
                            int64_t slots, int n_seg, const int32_t* seg_slot, float* bias, void* stream) {
   if (!q || !q8 || !q_scale) return LBW_E_NULL;
+  if (dtype != LBW_DTYPE_BF16 && dtype != LBW_DTYPE_FP16) return LBW_E_SHAPE;
   if (batch <= 0 || heads <= 0 || lq <= 0 || batch * heads > 65535) return LBW_E_SHAPE;
   if (n_seg < 0 || n_seg > LBW_MAX_SEGMENTS) return LBW_E_SEGMENTS;
   if (s_batch % 8 || s_tok % 8 || s_head % 8) return LBW_E_ALIGN;
@@ -116,8 +118,13 @@ extern "C" int lbw_quant_q(const uint16_t* q, int64_t batch, int64_t lq, int64_t
   }
   if (a.lp / QG > 0x7fffffff) return LBW_E_SHAPE;
   if (const int dv = check_device()) return dv;
-  hipLaunchKernelGGL(quant_q_kernel, dim3((unsigned)(a.lp / QG), (unsigned)((a.bh + QQ_WAVES - 1) / QQ_WAVES)),
-                     dim3(64 * QQ_WAVES), 0, (hipStream_t)stream, q, a, q8, q_scale, km, bias);
+  const dim3 grid((unsigned)(a.lp / QG), (unsigned)((a.bh + QQ_WAVES - 1) / QQ_WAVES));
+  if (dtype == LBW_DTYPE_FP16)
+    hipLaunchKernelGGL(quant_q_kernel<true>, grid, dim3(64 * QQ_WAVES), 0, (hipStream_t)stream, q, a, q8, q_scale, km,
+                       bias);
+  else
+    hipLaunchKernelGGL(quant_q_kernel<false>, grid, dim3(64 * QQ_WAVES), 0, (hipStream_t)stream, q, a, q8, q_scale,
+                       km, bias);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }

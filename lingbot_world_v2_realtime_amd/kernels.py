@@ -35,6 +35,18 @@ def _require_cuda_bf16(name, t):
         raise ValueError(f"{name} must have a contiguous head dim of {HEAD_DIM}, got shape {tuple(t.shape)}")
 
 
+DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1}   # LBW_DTYPE_BF16 / LBW_DTYPE_FP16 of include/lbw_attn.h
+
+
+def _require_cuda_16(name, t):
+    """A device tensor of bf16 or fp16 with a contiguous 128-wide head dim (the quantisers' inputs); returns the
+    format code the C-ABI takes."""
+    if t.dtype not in DTYPE_CODE:
+        raise TypeError(f"{name} must be bfloat16 or float16, got {t.dtype}")
+    _require_cuda_bf16(name, t.view(torch.bfloat16) if t.dtype == torch.float16 else t)
+    return DTYPE_CODE[t.dtype]
+
+
 def _same_device(what, *tensors):
     """Every tensor (None skipped) on one device: a kernel launched on the current device would otherwise read or
     write another GPU's memory through a raw pointer."""
@@ -89,14 +101,15 @@ def requant_workspace(layers, bh, length, device):
 
 
 def kv_requant(k, v, ring, slot, layer0=0, workspace=None):
-    """Quantise bf16 K, V chunks into `slot` of `ring`.
+    """Quantise bf16 (or fp16) K, V chunks into `slot` of `ring`.
 
     k, v: [B, L, H, 128] (one layer; written to layer `layer0`) or [layers, B, L, H, 128] (layers
     layer0 .. layer0 + layers - 1), any strides with a contiguous head dim.
     """
     lib = _lib.load()
-    _require_cuda_bf16("k", k)
-    _require_cuda_bf16("v", v)
+    dtype = _require_cuda_16("k", k)
+    if _require_cuda_16("v", v) != dtype:
+        raise TypeError(f"k ({k.dtype}) and v ({v.dtype}) must have one dtype")
     if k.shape != v.shape:
         raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
     _same_device("kv_requant", k, v, ring.k8, workspace)
@@ -110,7 +123,7 @@ def kv_requant(k, v, ring, slot, layer0=0, workspace=None):
         workspace = requant_workspace(nl, b * h, n, k.device)
     ks, vs = k.stride(), v.stride()
     st = lib.lbw_kv_requant(
-        _ptr(k), _ptr(v), nl, b, n, h, ks[0], ks[1], ks[2], ks[3], vs[0], vs[1], vs[2], vs[3],
+        _ptr(k), _ptr(v), dtype, nl, b, n, h, ks[0], ks[1], ks[2], ks[3], vs[0], vs[1], vs[2], vs[3],
         _ptr(ring.k8[layer0]), _ptr(ring.k_scale[layer0]), _ptr(ring.km[layer0]), _ptr(ring.v8[layer0]),
         _ptr(ring.v8lo[layer0]) if ring.v8lo is not None else None, _ptr(ring.v_scale[layer0]),
         ring.slots, ring.cap, slot, _ptr(workspace), _stream(k))
@@ -118,9 +131,9 @@ def kv_requant(k, v, ring, slot, layer0=0, workspace=None):
 
 
 def quant_q(q, layout="NHD", ring=None, layer=0, seg_slots=()):
-    """bf16 Q -> (q8 [BH, Lp, 128], q_scale [BH, Lp/32], bias [n_seg, BH, Lp] or None)."""
+    """bf16 / fp16 Q -> (q8 [BH, Lp, 128], q_scale [BH, Lp/32], bias [n_seg, BH, Lp] or None)."""
     lib = _lib.load()
-    _require_cuda_bf16("q", q)
+    dtype = _require_cuda_16("q", q)
     b, lq, h, s_b, s_t, s_h = _dims(q, layout)
     if len(seg_slots) > 1:
         _same_device("quant_q", q, ring.km)
@@ -134,7 +147,7 @@ def quant_q(q, layout="NHD", ring=None, layer=0, seg_slots=()):
         bias = torch.empty(n_seg, bh, lp, dtype=torch.float32, device=q.device)
         km_ptr, slots = _ptr(ring.km[layer]), ring.slots
         seg_arr = (ctypes_i32 * n_seg)(*seg_slots)
-    st = lib.lbw_quant_q(_ptr(q), b, lq, h, s_b, s_t, s_h, _ptr(q8), _ptr(qs), km_ptr, slots, n_seg,
+    st = lib.lbw_quant_q(_ptr(q), dtype, b, lq, h, s_b, s_t, s_h, _ptr(q8), _ptr(qs), km_ptr, slots, n_seg,
                          seg_arr, _ptr(bias), _stream(q))
     _lib.check(st, "lbw_quant_q")
     return q8, qs, bias

@@ -43,16 +43,14 @@ def sage_attention(q, k, v, tensor_layout="NHD", is_causal=False, sm_scale=None)
     """Quantized attention, the call `sageattn(q, k, v, tensor_layout, is_causal, sm_scale)` makes on sm_120
     (per-warp int8 Q, mean-smoothed per-block int8 K, per-channel fp8 V; lingbot/layers/attention.py:34-35).
 
-    q [B, Lq, H, 128], k/v [B, Lk, H, 128] for "NHD" ([B, H, L, 128] for "HND"), bf16 (or fp16, rounded to bf16
-    first: the quantisers read bf16) on the GPU. Returns bf16 in q's layout. The K mean and V scales are taken over
-    all Lk keys (one chunk), so the logits need no per-chunk bias. Raises if liblbw_attn.so is missing: there is no
-    fallback.
+    q [B, Lq, H, 128], k/v [B, Lk, H, 128] for "NHD" ([B, H, L, 128] for "HND"), bf16 or fp16 (quantised from
+    their own format) on the GPU. Returns bf16 in q's layout. The K mean and V scales are taken over all Lk keys
+    (one chunk), so the logits need no per-chunk bias. Raises if liblbw_attn.so is missing: there is no fallback.
     """
     if is_causal:
         raise NotImplementedError("the quantized kernel is non-causal; the DiT never calls it causally")
-    q, k, v = (t.to(torch.bfloat16) if t.dtype == torch.float16 else t for t in (q, k, v))
     for name, t in (("q", q), ("k", k), ("v", v)):
-        kernels._require_cuda_bf16(name, t)
+        kernels._require_cuda_16(name, t)
     b, lq, h, *_ = kernels._dims(q, tensor_layout)
     bk, lk, hk, *_ = kernels._dims(k, tensor_layout)
     if (bk, hk) != (b, h) or tuple(v.shape) != tuple(k.shape):
@@ -62,7 +60,7 @@ def sage_attention(q, k, v, tensor_layout="NHD", is_causal=False, sm_scale=None)
     ring, ws = _dropin_buffers(b, h, lk, q.device)
     kernels.kv_requant(k, v, ring, 0, workspace=ws)
     q8, qs, _ = kernels.quant_q(q, tensor_layout)
-    out = torch.empty_like(q)
+    out = torch.empty_like(q, dtype=torch.bfloat16)
     return kernels.attn_fwd(q8, qs, None, b, lq, h, ring, 0, [0], [lk], out, tensor_layout, sm_scale)
 
 
@@ -138,8 +136,8 @@ def cross_attention(q, cache, k_lens=None, softmax_scale=None):
 def attention(q, k, v, q_lens=None, k_lens=None, dropout_p=0., softmax_scale=None, q_scale=None,
               causal=False, window_size=(-1, -1), deterministic=False, dtype=None, fa_version=None):
     """Drop-in for lingbot/layers/attention.py:27-40: same arguments, same routing, q.dtype out. Inputs are cast
-    to `dtype` (bf16 by default) as the reference does before its Sage call; an fp16 `dtype` is then rounded to
-    bf16 inside sage_attention. A causal call takes the SDPA route: the quantized kernel is non-causal (the
+    to `dtype` (bf16 by default) as the reference does before its Sage call, and quantised from that format (bf16 or
+    fp16). A causal call takes the SDPA route: the quantized kernel is non-causal (the
     reference hands causal to Sage; the DiT never calls it causally)."""
     dtype = torch.bfloat16 if dtype is None else dtype
     if _QUANT and q_lens is None and k_lens is None and dropout_p == 0. and not causal:

@@ -21,6 +21,8 @@ forward can be captured in a HIP graph. Two ways to choose what a forward attend
   tokens of chunk 1, the two latest saved chunks and the current chunk (27144 keys in 5 slots), and with
   `--local_attn_size 17` the rolling part starts 1508 tokens into the older of its two chunks.
 """
+import torch
+
 from .. import kernels
 
 __all__ = ["QuantKVRing", "alloc_cache", "save_chunk", "attend"]
@@ -197,13 +199,14 @@ class QuantKVRing:
         return [s for s, _, _ in ranges], [c for _, _, c in ranges], [a for _, a, _ in ranges]
 
     def attend(self, q, layer, sm_scale=None):
-        """Attention of q [B, Lq, H, 128] bf16 over the saved chunks plus the current one of `layer`."""
+        """Attention of q [B, Lq, H, 128] (bf16 or fp16) over the saved chunks plus the current one of `layer`;
+        bf16 out."""
         b, lq, h, _ = q.shape
         slots, lens, firsts = self.attended()
         if any(n == 0 for n in lens):
             raise RuntimeError("the current chunk has no K/V yet: call write() first")
         q8, qs, bias = kernels.quant_q(q, "NHD", self.cache, layer, slots)
-        out = q.new_empty(q.shape)
+        out = q.new_empty(q.shape, dtype=torch.bfloat16)
         return kernels.attn_fwd(q8, qs, bias, b, lq, h, self.cache, layer, slots, lens, out, "NHD", sm_scale,
                                 seg_firsts=firsts)
 

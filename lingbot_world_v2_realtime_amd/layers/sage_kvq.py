@@ -25,12 +25,12 @@ _KEYS = ("lbw_ring", "lbw_ws")
 
 def alloc_cache(shape, dtype, device):
     """Quantised buffers for one layer's cache dict; `shape` = [B, kv_size, H, D] (sage_kvq.py:38-48). `dtype` is
-    the dtype of the bf16 window the slice is quantised from (the kernels take bfloat16)."""
+    the dtype of the window the slice is quantised from: bfloat16 or float16."""
     b, kv_size, h, d = shape
     if d != kernels.HEAD_DIM:
         raise ValueError(f"head dim must be {kernels.HEAD_DIM}, got {d}")
-    if dtype != torch.bfloat16:
-        raise TypeError(f"the quantised cache is filled from bfloat16 K/V, got {dtype}")
+    if dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"the quantised cache is filled from bfloat16 or float16 K/V, got {dtype}")
     ring = kernels.RingCache(1, b, h, kernels.pad_to(kv_size, kernels.K_BLOCK), 1, device)
     return {"lbw_ring": ring, "lbw_ws": kernels.requant_workspace(1, b * h, kv_size, ring.device)}
 
@@ -60,12 +60,12 @@ def write_chunk(cache, start, end):
 
 
 def attend(q, cache, kv_len, sm_scale=None):
-    """Attention of q [B, Lq, H, D] (NHD, bf16) over the quantised slice's first kv_len tokens, only Q quantised
-    here (sage_kvq.py:101-111) -> [B, Lq, H, D] bf16."""
+    """Attention of q [B, Lq, H, D] (NHD, bf16 or fp16) over the quantised slice's first kv_len tokens, only Q
+    quantised here (sage_kvq.py:101-111) -> [B, Lq, H, D] bf16."""
     ring = cache["lbw_ring"]
     if not 1 <= kv_len <= ring.cap:
         raise ValueError(f"kv_len {kv_len} outside the cache (1..{ring.cap})")
     b, lq, h, _ = q.shape
     q8, qs, _ = kernels.quant_q(q, "NHD")
-    out = torch.empty_like(q)
+    out = torch.empty_like(q, dtype=torch.bfloat16)
     return kernels.attn_fwd(q8, qs, None, b, lq, h, ring, 0, [0], [kv_len], out, "NHD", sm_scale)

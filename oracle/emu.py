@@ -8,8 +8,9 @@ quantisers and its documentation of the fused kernel:
 - Q: int8 per 32-row group of 128-row tiles, scale = amax / 127, amax floored at 1e-7, values
   x * (127 / amax) in fp32, round half to even, saturate; rows past Lq count as zero
   (experiments/modules/sage_kvq.py:57-66, :104; rounding statement :14-19).
-- K: subtract the per-(head, channel) mean over the chunk, rounded to bf16 as `k.mean(dim=1)` on a bf16
-  tensor is (lingbot/layers/sage_preq.py:115; sage_kvq.py:85, :96), then int8 per 64-token block as above;
+- K: subtract the per-(head, channel) mean over the chunk, rounded to the input's dtype (bf16, or fp16) as
+  `k.mean(dim=1)` on such a tensor is (lingbot/layers/sage_preq.py:115; sage_kvq.py:85, :96), then int8 per
+  64-token block as above;
   tokens past the chunk count as zero after the subtraction (sage_kvq.py:61-63).
 - V: fp8 e4m3 with one scale per (head, channel) (sage_kvq.py:69-75; sage_preq.py:47-78). The reference maps
   amax to 2.25 because its PV accumulates in fp16 (sage_kvq.py:30-31); the MFMA here accumulates in fp32, so
@@ -34,7 +35,8 @@ In fp32, every sum starting from +0 and running left to right:
   B[b]     = H[b, 0] + H[b, 1]
   U[u]     = B[4u] + B[4u + 1] + B[4u + 2] + B[4u + 3]     (the blocks that exist)
   total    = U[0] + U[1] + ... + U[nsup - 1]
-  mean     = total / n (fp32, correctly rounded), km = bf16(mean) round to nearest even.
+  mean     = total / n (fp32, correctly rounded), km = mean rounded to nearest even in the input's dtype
+             (bf16, or fp16 for fp16 K).
 Padding tokens past n add +0.
 
 fp8 V layout per 64-key block: [channel][64 positions]; position p holds key
@@ -122,8 +124,10 @@ def quant_q(q):
     return q8.view(h, lp, d), qs
 
 
-def chunk_mean(k):
-    """Per-(head, channel) mean of k bf16 [L, H, D] in the fixed order above -> fp32 [H, D] holding bf16 values."""
+def chunk_mean(k, rounded=True):
+    """Per-(head, channel) mean of k bf16 / fp16 [L, H, D] in the fixed order above -> fp32 [H, D] holding values
+    of k's dtype (the mean is rounded to it, as `k.mean(dim=1)` on a bf16 or fp16 tensor is); rounded=False returns
+    the fp32 mean before that rounding."""
     k = _as_lhd(k)
     n, h, d = k.shape
     nb = pad_to(n, K_BLOCK) // K_BLOCK
@@ -144,7 +148,9 @@ def chunk_mean(k):
             sup = sup + blk[b]
         tot = tot + sup
     mean = tot / torch.tensor(float(n), dtype=torch.float32)
-    return bf16_round(mean)
+    if not rounded:
+        return mean
+    return mean.to(k.dtype).to(torch.float32) if k.dtype in (torch.bfloat16, torch.float16) else bf16_round(mean)
 
 
 def quant_k(k, km):

@@ -68,11 +68,11 @@ def test_requant_workspace_formula(lib):
 
 
 def requant(lib, **kw):
-    a = dict(k=FAKE, v=FAKE, layers=1, batch=1, len=100, heads=2, ks=(0, 0, 256, 128), vs=(0, 0, 256, 128),
-             k8=FAKE, k_scale=FAKE, km=FAKE, v8=FAKE, v8lo=None, v_scale=FAKE, slots=4, cap=128, slot=0,
-             ws=FAKE)
+    a = dict(k=FAKE, v=FAKE, dtype=0, layers=1, batch=1, len=100, heads=2, ks=(0, 0, 256, 128),
+             vs=(0, 0, 256, 128), k8=FAKE, k_scale=FAKE, km=FAKE, v8=FAKE, v8lo=None, v_scale=FAKE, slots=4, cap=128,
+             slot=0, ws=FAKE)
     a.update(kw)
-    return lib.lbw_kv_requant(a["k"], a["v"], a["layers"], a["batch"], a["len"], a["heads"], *a["ks"], *a["vs"],
+    return lib.lbw_kv_requant(a["k"], a["v"], a["dtype"], a["layers"], a["batch"], a["len"], a["heads"], *a["ks"], *a["vs"],
                               a["k8"], a["k_scale"], a["km"], a["v8"], a["v8lo"], a["v_scale"], a["slots"],
                               a["cap"], a["slot"], a["ws"], None)
 
@@ -88,13 +88,14 @@ def test_requant_argument_checks(lib):
     assert requant(lib, ks=(0, 0, 256, 129)) == E_ALIGN
     assert requant(lib, k8=FAKE + 8) == E_ALIGN
     assert requant(lib, v8lo=FAKE + 4) == E_ALIGN
+    assert requant(lib, dtype=2) == E_SHAPE            # bf16 (0) or fp16 (1) only
 
 
 def quant_q(lib, **kw):
-    a = dict(q=FAKE, batch=1, lq=100, heads=2, st=(0, 256, 128), q8=FAKE, qs=FAKE, km=FAKE, slots=4, n_seg=0,
-             seg=None, bias=FAKE)
+    a = dict(q=FAKE, dtype=0, batch=1, lq=100, heads=2, st=(0, 256, 128), q8=FAKE, qs=FAKE, km=FAKE, slots=4,
+             n_seg=0, seg=None, bias=FAKE)
     a.update(kw)
-    return lib.lbw_quant_q(a["q"], a["batch"], a["lq"], a["heads"], *a["st"], a["q8"], a["qs"], a["km"],
+    return lib.lbw_quant_q(a["q"], a["dtype"], a["batch"], a["lq"], a["heads"], *a["st"], a["q8"], a["qs"], a["km"],
                            a["slots"], a["n_seg"], a["seg"], a["bias"], None)
 
 
@@ -107,6 +108,7 @@ def test_quant_q_argument_checks(lib):
     assert quant_q(lib, n_seg=2, seg=None) == E_NULL
     assert quant_q(lib, n_seg=2, seg=seg) == E_SEGMENTS   # slot 5 of a 4-slot cache
     assert quant_q(lib, n_seg=2, seg=seg, km=FAKE + 4) == E_ALIGN   # the K means are read as float4
+    assert quant_q(lib, dtype=-1) == E_SHAPE
 
 
 ROPE_ROWS = 1024

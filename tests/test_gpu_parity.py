@@ -464,16 +464,43 @@ def test_dropin_keeps_one_ring_per_stream():
     assert torch.equal(a1, a3) and not torch.equal(a1, a2)
 
 
-def test_dropin_fp16_inputs_round_to_bf16():
-    """fp16 inputs (what attention(..., dtype=torch.float16) hands over) are rounded to bf16 before quantisation:
-    the same bits as the call on the bf16-rounded tensors."""
+@pytest.mark.parametrize("n", [1, 65, 1508])
+def test_requant_and_quant_q_fp16_bit_exact(n):
+    """fp16 K / V / Q (what attention(..., dtype=torch.float16) hands over) are quantised from their own format:
+    the K mean rounded to fp16, and every ring field and the int8 Q with its scales bit-exact against the oracle on
+    the same fp16 tensors."""
+    torch.manual_seed(n + 5)
+    h = 3
+    k = (torch.randn(1, n, h, 128) + 3 * torch.randn(1, 1, h, 128)).half()
+    v = (torch.randn(1, n, h, 128) * 1.7).half()
+    q = (torch.randn(1, n, h, 128) * 2).half()
+    ring = _ring(1, h, n, slots=1)
+    _k().kv_requant(k.to(DEV), v.to(DEV), ring, slot=0)
+    q8, qs, _ = _k().quant_q(q.to(DEV))
+    torch.cuda.synchronize()
+    ref = emu.requant(k, v)
+    assert not torch.equal(ref["km"], emu.requant(k.bfloat16(), v.bfloat16())["km"])   # fp16 rounding of the mean
+    _check_chunk(ring, 0, 0, ref, n)
+    r8, rs = emu.quant_q(q)
+    assert torch.equal(q8.cpu(), r8) and torch.equal(qs.cpu(), rs)
+
+
+def test_dropin_fp16_inputs():
+    """The drop-in on fp16 q / k / v: bf16 out, against the oracle run on the same fp16 tensors and fp32 SDPA."""
     from lingbot_world_v2_realtime_amd import sage_attention
     q, k, v, _ = emu.make_inputs(300, 500, h=2, seed=74)
-    qh, kh, vh = (x.float().half().to(DEV) for x in (q, k, v))
-    got = sage_attention(qh, kh, vh)
-    want = sage_attention(*(x.to(torch.bfloat16) for x in (qh, kh, vh)))
+    q, k, v = (x.float().half() for x in (q, k, v))
+    out = sage_attention(q.to(DEV), k.to(DEV), v.to(DEV))
     torch.cuda.synchronize()
-    assert got.dtype == torch.bfloat16 and torch.equal(got, want)
+    assert out.dtype == torch.bfloat16
+    out = out.float().cpu()
+    ref = emu.attention(q, [emu.requant(k, v)], schedule_gx=_gx())[None]
+    sd = emu.sdpa_fp32(q, k, v)[None]
+    e_emu, e_sd, e_scheme = (out - ref).abs(), (out - sd).abs(), (ref - sd).abs()
+    record(f"drop-in fp16 inputs (300 q x 500 k) vs oracle mean {e_emu.mean():.3e}; vs fp32 SDPA max "
+           f"{e_sd.max():.3e} mean {e_sd.mean():.3e}; oracle vs SDPA mean {e_scheme.mean():.3e}")
+    assert e_emu.mean() <= 0.1 * e_scheme.mean() + 2e-3 * sd.abs().mean()
+    assert e_sd.mean() <= 1.1 * e_scheme.mean() + 1e-5
 
 
 def test_hnd_layout_same_bits():

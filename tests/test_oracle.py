@@ -97,7 +97,9 @@ def test_last_group_counts_padding_as_zero():
 # ---------------------------------------------------------------- K mean (fixed order) and smoothing
 
 def mean_by_loops(k):
-    """The documented mean order, restated with scalar fp32 loops (tiny inputs only)."""
+    """The documented mean order, restated with scalar fp32 loops (tiny inputs only): 4-token sums, eight of them
+    per 32-token half left to right, the two halves added, the blocks of each 4-block super-block left to right,
+    the super-blocks left to right, then / n. Returns the fp32 mean (before any rounding)."""
     n, h, d = k.shape
     nb = (n + 63) // 64
     out = np.zeros((h, d), dtype=np.float32)
@@ -109,26 +111,35 @@ def mean_by_loops(k):
             for u in range(0, nb, 4):
                 sup = np.float32(0)
                 for b in range(u, min(nb, u + 4)):
-                    blk = np.float32(0)
-                    for q in range(16):
-                        s = np.float32(0)
-                        for j in range(4):
-                            s = np.float32(s + x[64 * b + 4 * q + j, hh, c])
-                        blk = np.float32(blk + s)
-                    sup = np.float32(sup + blk)
+                    halves = []
+                    for i in range(2):
+                        half = np.float32(0)
+                        for q in range(8 * i, 8 * i + 8):
+                            s = np.float32(0)
+                            for j in range(4):
+                                s = np.float32(s + x[64 * b + 4 * q + j, hh, c])
+                            half = np.float32(half + s)
+                        halves.append(half)
+                    sup = np.float32(sup + np.float32(halves[0] + halves[1]))
                 tot = np.float32(tot + sup)
             out[hh, c] = np.float32(tot / np.float32(n))
-    return torch.from_numpy(out).to(torch.bfloat16).float()
+    return torch.from_numpy(out)
 
 
-def test_chunk_mean_order_and_accuracy():
+@pytest.mark.parametrize("dtype,mant", [(torch.bfloat16, 7), (torch.float16, 10)])
+def test_chunk_mean_order_and_accuracy(dtype, mant):
+    """The fp32 mean bit for bit against the scalar-loop restatement of the documented order (values with many
+    mantissa bits, so a different order would round differently), and the rounded mean within one ulp of the
+    input format (bf16, fp16) of the fp64 mean."""
     torch.manual_seed(2)
-    k = (torch.randn(700, 2, 4) * 3 + torch.tensor([1e3, -7.0, 0.01, 50.0])).to(torch.bfloat16)
+    scale = torch.tensor([1e3, -7.0, 0.01, 50.0]) if dtype == torch.bfloat16 else torch.tensor([300.0, -7.0, 0.01, 50.0])
+    k = (torch.randn(700, 2, 4) * 3 + scale).to(dtype)
+    assert torch.equal(emu.chunk_mean(k, rounded=False), mean_by_loops(k))
     km = emu.chunk_mean(k)
-    assert torch.equal(km, mean_by_loops(k))
+    assert torch.equal(km, mean_by_loops(k).to(dtype).float())
     exact = k.double().mean(dim=0)
-    ulp = torch.tensor([2.0 ** (math.floor(math.log2(abs(v))) - 7) for v in exact.flatten().tolist()]).view(2, 4)
-    assert torch.all((km.double() - exact).abs() <= ulp)              # within one bf16 ulp of the true mean
+    ulp = torch.tensor([2.0 ** (math.floor(math.log2(abs(v))) - mant) for v in exact.flatten().tolist()]).view(2, 4)
+    assert torch.all((km.double() - exact).abs() <= ulp)              # within one ulp of the true mean
 
 
 def test_smoothing_makes_k8_invariant_to_channel_offsets():
