@@ -69,13 +69,15 @@ def attention_ops(lq, lk, h=H, d=D, b=1):
     return 4.0 * b * h * lq * lk * d
 
 
-def requant_bytes(n, h=H, d=D, v_planes=1):
+def requant_bytes(n, h=H, d=D, v_planes=1, v_table=False):
     """Bytes of one chunk's K/V re-quant: bf16 K and V read once; int8 K and `v_planes` e4m3 V planes written
     once; one fp32 scale per 64-token K block; fp32 mean and V scale per (head, channel). With one V plane this
     is the algorithmic count (55,607,760 B per layer at 6032 tokens x 12 heads); the second (residual) plane
-    this build also writes is overhead on top of it."""
+    this build also writes is overhead on top of it, and so is its V scale table (v_table: 256 B per 64-token
+    block and head in place of the per-channel fp32 V scale)."""
     nb = (n + 63) // 64
-    return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + 2 * h * d * 4
+    v_scale = nb * h * 256 if v_table else h * d * 4
+    return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + h * d * 4 + v_scale
 
 
 def _profile(name):
@@ -561,7 +563,7 @@ def main():
         rq.write_layers(kl, vl)
     rq_ms = _timed(lambda: rq.write_layers(kl, vl), 10, stream)
     rq_bytes = LAYERS * requant_bytes(CHUNK, H, D)
-    rq_moved = LAYERS * requant_bytes(CHUNK, H, D, v_planes=2)
+    rq_moved = LAYERS * requant_bytes(CHUNK, H, D, v_planes=2, v_table=True)
     rq_gbps = rq_bytes / (rq_ms * 1e-3) / 1e9
     del kl, vl, rq
 

@@ -22,10 +22,13 @@
  *   k_scale fp32  [layers][slots][BH][nb]             amax / 127 of each 64-token block
  *   km      fp32  [layers][slots][BH][128]            per-(head, channel) chunk mean (a bf16 value)
  *   v8      uint8 [layers][slots][BH][nb][128][64]    e4m3 V, per 64-key block: [channel][position]
- *   v8lo    uint8 [layers][slots][BH][nb][128][64]    optional second e4m3 plane: (y - hi) * 16, y = V / v_scale
- *   v_scale fp32  [layers][slots][BH][128]            per (head, channel): the power of two 2^e with amax / 2^e
- *                                                      in (224, 448] (amax floored at 1e-7), so y is exact
- * With the second plane, V = (hi + lo / 16) * v_scale to about 7 significant bits instead of 4.
+ *   v8lo    uint8 [layers][slots][BH][nb][128][64]    optional second e4m3 plane: (y - hi) * 16, y = V / 2^e
+ *   v_scale uint8 [layers][slots][BH][nb][256]        E8M0 V scales of each 64-key block: one power of two 2^e per
+ *                                                      (key group, channel) with amax / 2^e in (224, 448] (amax over
+ *                                                      the group's 32 keys, floored at 1e-7), so y is exact; byte
+ *                                                      (32 g + c % 32) * 4 + c / 32 = 127 + e of channel c, group g
+ * Key k of a block is in group k / 32 (its 32-key half).
+ * With the second plane, V = (hi + lo / 16) * 2^e to about 7 significant bits instead of 4.
  * Position p of a 64-key V block holds key 32*((p&31)>>4) + 8*((p>>2)&3) + 4*(p>>5) + (p&3).
  *
  * Quantised Q (per call): q8 int8 [BH][Lp][128], q_scale fp32 [BH][Lp/32], Lp = Lq rounded up to 256;
@@ -71,7 +74,7 @@ int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len);
  * Quantise K and V chunks of `len` tokens (bf16, or fp16 with dtype LBW_DTYPE_FP16: 16-bit words either way) into
  * slot `slot` of `layers` consecutive layer caches: the per-(head, channel) K mean (rounded to the inputs' own
  * format, as the reference's k.mean of such a tensor), K - mean as int8 per 64-token block, V as e4m3 with one scale
- * per (head, channel), plus the residual plane when v8lo is not null. Replaces sage_kvq.requant_all + write_chunk (experiments/modules/sage_kvq.py:78-98)
+ * per (64-key block, key group, channel), plus the residual plane when v8lo is not null. Replaces sage_kvq.requant_all + write_chunk (experiments/modules/sage_kvq.py:78-98)
  * and Sage's per_warp_int8 K part / per_channel_fp8 (lingbot/layers/sage_preq.py:115-124).
  * k/v element (layer l, batch b, token t, head h, channel d) sits at l*s_layer + b*s_batch + t*s_tok
  * + h*s_head + d. `workspace` holds lbw_kv_requant_workspace_bytes() bytes, 16-byte aligned; its
@@ -82,7 +85,7 @@ int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int dtype,
                    int64_t layers, int64_t batch, int64_t len, int64_t heads,
                    int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok, int64_t k_s_head,
                    int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
-                   int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,
+                   int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, uint8_t* v_scale,
                    int64_t slots, int64_t cap, int64_t slot,
                    void* workspace, void* stream);
 
@@ -133,7 +136,7 @@ int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, int64_t batch
                              const double* rope, int64_t rope_rows, int64_t grid_h, int64_t grid_w,
                              int64_t start_frame, uint16_t* k_out, int64_t o_s_batch, int64_t o_s_tok,
                              int64_t o_s_head, int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo,
-                             float* v_scale, int64_t slots, int64_t cap, int64_t slot, void* workspace,
+                             uint8_t* v_scale, int64_t slots, int64_t cap, int64_t slot, void* workspace,
                              void* stream);
 
 /*
@@ -188,9 +191,9 @@ int lbw_quant_mx_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t rows_pa
  * chunk's first and last 64-token blocks outside that range are masked, so a window may start and end anywhere
  * in a chunk (the token window of lingbot/layers/kv_cache.py:23-81). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the
- * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA (a second fp8 product with the
- * residual plane, scaled by 2^-4, when v8lo is not null), fp32 accumulation, V scale
- * and 1 / row sum applied at the end. Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
+ * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA with V's E8M0 block scales applied by
+ * the MFMA itself (a second fp8 product with the residual plane, scaled 2^-4 lower, when v8lo is not null), fp32
+ * accumulation, 1 / row sum applied at the end. Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
  * 126-127; experiments/modules/sage_kvq.py:107-110). seg_slot / seg_len are host arrays. `workspace` holds
  * lbw_attn_workspace_bytes() bytes (16-byte aligned); two kernels run: the attention over a persistent grid
  * and a merge of the query tiles whose keys were split between workgroups.
@@ -198,7 +201,7 @@ int lbw_quant_mx_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t rows_pa
 int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias,
                  int64_t batch, int64_t lq, int64_t heads,
                  const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
-                 const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                 const uint8_t* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
                  const int32_t* seg_len, const int32_t* seg_first,
                  uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
                  float sm_scale, void* workspace, void* stream);
@@ -221,7 +224,7 @@ int64_t lbw_attn_workspace_bytes(void);
 int lbw_attn_fwd_noalloc(const int8_t* q8, const float* q_scale, const float* bias,
                          int64_t batch, int64_t lq, int64_t heads,
                          const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
-                         const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                         const uint8_t* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
                          const int32_t* seg_len, const int32_t* seg_first,
                          uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
                          float sm_scale, void* stream);
@@ -249,7 +252,7 @@ int lbw_attn_workgroups_per_xcd(void);
 int lbw_qk_logits_i32(const int8_t* q8, const float* q_scale, const float* bias,
                       int64_t batch, int64_t lq, int64_t heads,
                       const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
-                      const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                      const uint8_t* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
                       const int32_t* seg_len, const int32_t* seg_first,
                       uint16_t* out, int64_t o_s_batch, int64_t o_s_tok, int64_t o_s_head,
                       float sm_scale, int32_t* logits, void* workspace, void* stream);

@@ -94,9 +94,8 @@ __device__ __forceinline__ float sum32(const float* p) {
 }
 
 struct Piece {      // online-softmax state of one wave after a range of key blocks
-  v16f o[4];        // O^T accumulator, units of the last chunk's V scale
+  v16f o[4];        // O^T accumulator, in true V units (the PV MFMAs apply V's block scales)
   float m, l;       // reference max (log2 domain, bias included) and row sum (both lane halves combined)
-  int c_last;       // chunk of the last block processed
 };
 
 // ---- 8-wave ping-pong attention --------------------------------------------------------------------------
@@ -107,7 +106,7 @@ struct Piece {      // online-softmax state of one wave after a range of key blo
 // one 1 KB piece of each tile of block j + LEAD into LDS with direct global -> LDS loads, through NSTAGE stages;
 // group A waits for its pieces at the end of a softmax phase, group B at the end of an MFMA phase (in the fast
 // form of the pass both groups wait at both points), so each block has landed before the barrier that opens its
-// first MFMA phase. Stage layout (24 KB):
+// first MFMA phase. Stage layout (24 KB, and the block's 256-byte V scale table in a table of its own):
 // K tile 64 rows x 128 B, V tile 128 channels x 64 B, V residual tile; 16-byte chunks XOR-swizzled by row
 // (K: chunk ^ ((row >> 1) & 7), V: chunk ^ ((row >> 2) & 3)) so that the fragment reads of the MFMA operands hit
 // 16 distinct bank groups per 16 lanes, and every 1 KB of a tile is one contiguous DMA of 64 lanes x 16 B.
@@ -117,16 +116,18 @@ constexpr int NSTAGE = 6;
 constexpr int LEAD = 4;                        // NSTAGE - LEAD >= 2: a stage is free one phase before its reload
 constexpr int ST_K = 0, ST_V = 8192, ST_VLO = 16384, ST_BYTES = 24576;
 static_assert(QT == 32 * AT_WAVES, "query tile");
-// Per-piece chunk tables after the stages, so a chunk switch inside the loop reads LDS instead of global
-// memory (waiting for a global load would also wait for every global -> LDS load in flight):
-//   ratio [chunk c][channel]  v_scale(c - 1) / v_scale(c), the factor that takes O to chunk c's V scale
+// Scales of the block in each stage ([stage][wave w][36 B]): wave w's record holds dwords 8 w .. 8 w + 7 of the
+// block's V scale table, then the block's K scale (each wave its own copy). Table dword l is the E8M0 block scales
+// lane l gives the PV MFMAs (byte mt: channel 32 mt + l % 32, keys 32 (l / 32) .. + 31 of the block -- the MFMA's
+// K-block l / 32, bytes 16 (l / 32) .. + 15 of every lane's operand). One 9-lane load per wave and block fills a
+// record, with the block's tiles.
+constexpr int SC_WAVE = 36, SC_STAGE = AT_WAVES * SC_WAVE;
+constexpr int TAB_SC = NSTAGE * ST_BYTES;
+// Per-piece chunk table, so a chunk switch inside the loop reads LDS instead of global memory (waiting for a
+// global load would also wait for every global -> LDS load in flight):
 //   bias  [chunk c][query]    q . mean_k(c) * sm_scale * log2(e) of the tile's queries
-constexpr int TAB_RATIO = NSTAGE * ST_BYTES;
-constexpr int TAB_BIAS = TAB_RATIO + LBW_MAX_SEGMENTS * D * 4;
-// K scale of the block in each stage, one copy per wave ([stage][wave]): it arrives by DMA with the block's
-// tiles, so the softmax reads it from LDS instead of waiting for a scalar load per block
-constexpr int TAB_KS = TAB_BIAS + LBW_MAX_SEGMENTS * QT * 4;
-constexpr int AT_LDS = TAB_KS + NSTAGE * AT_WAVES * 4;   // 159936 of the 163840 bytes of a CU
+constexpr int TAB_BIAS = TAB_SC + NSTAGE * SC_STAGE;
+constexpr int AT_LDS = TAB_BIAS + LBW_MAX_SEGMENTS * QT * 4;   // 157376 of the 163840 bytes of a CU
 static_assert(AT_LDS <= 163840, "LDS");
 
 // Workgroup barrier that also stops the compiler from moving memory accesses across it. No wait is implied:
@@ -138,17 +139,17 @@ __device__ __forceinline__ void phase_barrier() {
 }
 
 // s_waitcnt on vmcnt only (lgkmcnt and expcnt at their maxima); vmcnt bits 5:4 sit in bits 15:14.
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 __device__ __forceinline__ void wait_vm(int n) {
-  switch (n) {
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-    case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
-    case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
-    case 16: __builtin_amdgcn_s_waitcnt(0x4F70); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F70); break;   // 0, and anything else: wait for everything
+  switch (n) {   // the counts the block loop uses: multiples of 3 or 4 DMA instructions per block, up to 4 blocks
+    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(vmcnt_imm(8)); break;
+    case 9: __builtin_amdgcn_s_waitcnt(vmcnt_imm(9)); break;
+    case 12: __builtin_amdgcn_s_waitcnt(vmcnt_imm(12)); break;
+    case 16: __builtin_amdgcn_s_waitcnt(vmcnt_imm(16)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;   // 0, and anything else: wait for everything
   }
 }
 
@@ -174,40 +175,49 @@ __device__ __forceinline__ v16i mfma_i8_from_magic(v4i a, v4i b) {
 }
 
 // A block's loads in one asm, M0 saved once and restored once around them: the K, V and (with TWO) V-residual tiles,
-// 16 bytes per lane, then the block's 4-byte K scale by lane 0 alone (EXEC set to lane 0 around that load and
-// restored before the asm ends, so no branch). Each source is a wave-uniform base plus a 32-bit per-lane byte
-// offset (the global instruction's scalar-base form: no 64-bit address per lane to form).
+// 16 bytes per lane, each a wave-uniform base plus a 32-bit per-lane byte offset (the global instruction's
+// scalar-base form: no 64-bit address per lane to form); then the wave's scale record by lanes 0-8 from 64-bit
+// per-lane addresses (`sp`: lanes 0-7 this wave's 32 bytes of the V scale table, lane 8 the K scale), lane i
+// writing M0 + 4 i (EXEC narrowed around that load and restored before the asm ends, so no branch).
 template <bool TWO>
 __device__ __forceinline__ void dma_block(const void* kb, uint32_t koff, const void* vb, const void* vlb, uint32_t voff,
-                                          const void* ksb, uint8_t* lk, uint8_t* lv, uint8_t* lvl, uint8_t* lks) {
+                                          uint64_t sp, uint8_t* lk, uint8_t* lv, uint8_t* lvl, uint8_t* lsc) {
   uint32_t keep;
   uint64_t ex;
-  const uint32_t zero = 0;
   if (TWO)
     asm volatile("s_mov_b32 %0, m0\n\t"
                  "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\t"
                  "s_mov_b32 m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %5\n\t"
                  "s_mov_b32 m0, %9\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %8\n\t"
-                 "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 1\n\t"
-                 "s_mov_b32 m0, %12\n\ts_nop 0\n\tglobal_load_lds_dword %10, %11\n\t"
+                 "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 0x1ff\n\t"
+                 "s_mov_b32 m0, %11\n\ts_nop 0\n\tglobal_load_lds_dword %10, off\n\t"
                  "s_mov_b64 exec, %1\n\t"
                  "s_mov_b32 m0, %0"
                  : "=&s"(keep), "=&s"(ex)
                  : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv)), "s"(vlb),
-                   "s"(lds_addr(lvl)), "v"(zero), "s"(ksb), "s"(lds_addr(lks))
+                   "s"(lds_addr(lvl)), "v"(sp), "s"(lds_addr(lsc))
                  : "memory");
   else
     asm volatile("s_mov_b32 %0, m0\n\t"
                  "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\t"
                  "s_mov_b32 m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %5\n\t"
-                 "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 1\n\t"
-                 "s_mov_b32 m0, %10\n\ts_nop 0\n\tglobal_load_lds_dword %8, %9\n\t"
+                 "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 0x1ff\n\t"
+                 "s_mov_b32 m0, %9\n\ts_nop 0\n\tglobal_load_lds_dword %8, off\n\t"
                  "s_mov_b64 exec, %1\n\t"
                  "s_mov_b32 m0, %0"
                  : "=&s"(keep), "=&s"(ex)
-                 : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv)), "v"(zero), "s"(ksb),
-                   "s"(lds_addr(lks))
+                 : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv)), "v"(sp),
+                   "s"(lds_addr(lsc))
                  : "memory");
+}
+
+// PV MFMA f of a block: O^T tile f & 3 += V^T fragment (hi plane for f < 4, the residual plane after) times P^T,
+// with V's E8M0 block scales from byte f & 3 of vsc (the byte select is an immediate of the instruction) and P
+// unscaled, or scaled by 2^-4 for the residual plane (a constant operand, so no per-block arithmetic on vsc).
+template <int F>
+__device__ __forceinline__ void pv_mfma(v16f (&o)[4], const v8i& vf, const v8i& pb, int vsc) {
+  o[F & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, o[F & 3], 0, 0, F & 3, vsc, 0,
+                                                             F < 4 ? E8M0_ONE : E8M0_LO);
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
@@ -218,9 +228,9 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
                                              const float* __restrict__ q_scale, const float* __restrict__ bias,
                                              const int8_t* __restrict__ k8, const float* __restrict__ k_scale,
                                              const uint8_t* __restrict__ v8, const uint8_t* __restrict__ v8lo,
-                                             const float* __restrict__ v_scale, uint8_t* lds, int bh, int64_t q0,
+                                             const uint8_t* __restrict__ v_scale, uint8_t* lds, int bh, int64_t q0,
                                              int j0, int j1, Piece& st, int32_t* __restrict__ logits) {
-  constexpr int NPB = TWO ? 4 : 3;   // DMA instructions per block of each wave (tiles + the K scale)
+  constexpr int NPB = TWO ? 4 : 3;   // DMA instructions per block of each wave (tiles, then the scale record)
   const int t = threadIdx.x, lane = t & 63, lq = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform, so the loader's control stays scalar
   const bool grp_a = w < 4;
@@ -266,20 +276,24 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   const int8_t* kbase;
   const uint8_t* vbase;
   const uint8_t* vlbase;
-  const float* ksbase;
+  // this lane's scale dword of the block (lanes 0-7: V scale table bytes 32 w + 4 lane ..; lane 8: the K scale; the
+  // other lanes load nothing) and its step to the next block of a chunk
+  uint64_t sptr;
+  const uint32_t sstep = lane < 8 ? 256u : 4u;
   auto seek = [&](int cc, int bb) {   // block bb of chunk cc's range, i.e. slot block seg_fb[cc] + bb
     const int64_t sbh = (int64_t)a.seg_slot[cc] * a.bh + bh;
     const int64_t blk = (int64_t)bb + a.seg_fb[cc];
     kbase = k8 + (sbh * a.cap + blk * KB) * D;
     vbase = v8 + (sbh * a.nbc + blk) * TILE_BYTES;
     if (TWO) vlbase = v8lo + (sbh * a.nbc + blk) * TILE_BYTES;
-    ksbase = k_scale + sbh * a.nbc + blk;
+    sptr = lane < 8 ? (uint64_t)(uintptr_t)(v_scale + (sbh * a.nbc + blk) * 256 + w * 32 + 4 * lane)
+                    : (uint64_t)(uintptr_t)(k_scale + sbh * a.nbc + blk);
   };
   seek(lc, lb);
   auto issue = [&](int stage) {
     uint8_t* sb = lds + stage * ST_BYTES + w * 1024;
-    dma_block<TWO>(kbase, (uint32_t)koff, vbase, TWO ? (const void*)vlbase : nullptr, (uint32_t)voff, ksbase,
-                   sb + ST_K, sb + ST_V, sb + ST_VLO, lds + TAB_KS + (stage * AT_WAVES + w) * 4);
+    dma_block<TWO>(kbase, (uint32_t)koff, vbase, TWO ? (const void*)vlbase : nullptr, (uint32_t)voff, sptr,
+                   sb + ST_K, sb + ST_V, sb + ST_VLO, lds + TAB_SC + stage * SC_STAGE + w * SC_WAVE);
   };
   auto advance = [&](auto fast) {   // fast: the next block is in the same chunk (lrem >= 2)
     if (!decltype(fast)::value && --lrem == 0) {   // the fast form's steps are taken off lrem after the run
@@ -292,7 +306,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       kbase += TILE_BYTES;
       vbase += TILE_BYTES;
       if (TWO) vlbase += TILE_BYTES;
-      ++ksbase;
+      sptr += sstep;
     }
   };
 
@@ -305,23 +319,14 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int c_prev = c;
   int jd = j0;                                         // LOGITS: tile-relative block of the softmax phase
 
-  // chunk tables: their global loads go out before the first blocks' DMA, so waiting for them waits for
-  // nothing else. The previous piece's readers are done: it ended with a workgroup barrier.
-  float* const ratio_tab = (float*)(lds + TAB_RATIO);
+  // chunk table: its global loads go out before the first blocks' DMA, so waiting for them waits for nothing
+  // else. The previous piece's readers are done: it ended with a workgroup barrier.
   float* const bias_tab = (float*)(lds + TAB_BIAS) + 32 * w + lq;   // this lane's query; [c * QT]
-  float tb[LBW_MAX_SEGMENTS], rnum[2], rden[2];
+  float tb[LBW_MAX_SEGMENTS];
   if (multi) {
 #pragma unroll
     for (int cc = 0; cc < LBW_MAX_SEGMENTS; ++cc)
       if (cc < a.n_seg) tb[cc] = bias[((int64_t)cc * a.bh + bh) * a.lp + q0 + lq];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int idx = t + AT_THREADS * r, cc = 1 + (idx >> 7), ch = idx & (D - 1);
-      if (cc < a.n_seg) {
-        rnum[r] = v_scale[((int64_t)a.seg_slot[cc - 1] * a.bh + bh) * D + ch];
-        rden[r] = v_scale[((int64_t)a.seg_slot[cc] * a.bh + bh) * D + ch];
-      }
-    }
   }
 
   const int npre = n < LEAD ? n : LEAD;
@@ -335,11 +340,6 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
 #pragma unroll
     for (int cc = 0; cc < LBW_MAX_SEGMENTS; ++cc)
       if (cc < a.n_seg) bias_tab[cc * QT] = tb[cc] * a.sl2;
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int idx = t + AT_THREADS * r, cc = 1 + (idx >> 7);
-      if (cc < a.n_seg) ratio_tab[idx + D] = rnum[r] / rden[r];   // [cc][ch] = [(cc - 1) * D + ch + D]
-    }
     beta = tb[0];
 #pragma unroll
     for (int cc = 1; cc < LBW_MAX_SEGMENTS; ++cc)
@@ -360,8 +360,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   int it = 0;
   // One pass: the MFMA phase of block it and the softmax phase of block it. The fast form assumes what holds for
   // most passes: the loader's block it + LEAD exists and lies in the loader's current chunk, and block it is
-  // neither the first nor the last block of its chunk (so no rescale to a new V scale, no key mask, no chunk
-  // step). It returns true after the last MFMA phase (it == n).
+  // neither the first nor the last block of its chunk (so no new logit bias, no key mask, no chunk step). It
+  // returns true after the last MFMA phase (it == n).
   auto pass = [&](auto fast) -> bool {
     constexpr bool FAST = decltype(fast)::value;
     // ---- MFMA phase: S of block it, P V of block it - 1 ----
@@ -381,12 +381,20 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       const v8i r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       return r;
     };
-    auto pv = [&](int f, const v8i& vf) {
-      if (f < 4)
-        st.o[f] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[f], 0, 0, 0, 0, 0, 0);
-      else   // residual plane, accumulated with block scale 2^-4
-        st.o[f & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, st.o[f & 3], 0, 0, 0, E8M0_LO, 0,
-                                                                      E8M0_ONE);
+    // V's block scales: this lane's dword of block it - 1's table (read below); byte mt scales the rows of O^T
+    // tile mt (A operand row l % 32 in K-block l / 32).
+    int vsc;
+    auto pv = [&](int f, const v8i& vf) {   // f is a constant once the loop below is unrolled
+      switch (f) {
+        case 0: pv_mfma<0>(st.o, vf, pb, vsc); break;
+        case 1: pv_mfma<1>(st.o, vf, pb, vsc); break;
+        case 2: pv_mfma<2>(st.o, vf, pb, vsc); break;
+        case 3: pv_mfma<3>(st.o, vf, pb, vsc); break;
+        case 4: pv_mfma<4>(st.o, vf, pb, vsc); break;
+        case 5: pv_mfma<5>(st.o, vf, pb, vsc); break;
+        case 6: pv_mfma<6>(st.o, vf, pb, vsc); break;
+        default: pv_mfma<7>(st.o, vf, pb, vsc); break;
+      }
     };
     // Both halves run on every pass, so the LDS waits need no control-flow joins: at it == n the QK MFMAs read
     // a stage nothing uses (its int32 results are dropped), and at it == 0 P is all zeros, so the PV MFMAs add
@@ -405,7 +413,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       }
     }
     // the K scale of block it, for its softmax in the next phase (this wave's copy landed with its pieces)
-    const float ks = *(const float*)(lds + TAB_KS + (stage * AT_WAVES + w) * 4);
+    const float ks = *(const float*)(lds + TAB_SC + stage * SC_STAGE + w * SC_WAVE + 32);
+    vsc = *(const int*)(lds + TAB_SC + pstage * SC_STAGE + (lane >> 3) * SC_WAVE + 4 * (lane & 7));
     if (do_pv) {
       vq[0] = vfrag(0);
       vq[1] = vfrag(1);
@@ -471,19 +480,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
 
     // ---- softmax phase for block it (chunk c) ----
     if (!FAST && c != c_prev) {
-      // a new chunk (c_prev == c - 1: every chunk has a block): O (blocks before this one) to its V scale,
-      // and its logit bias, both from the piece's LDS tables
-      const float* rt = ratio_tab + c * D + 4 * g;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {   // channels 32 mt + 8 q + 4 g + (0..3)
-          const float4 r = *(const float4*)(rt + 32 * mt + 8 * q);
-          st.o[mt][4 * q] *= r.x;
-          st.o[mt][4 * q + 1] *= r.y;
-          st.o[mt][4 * q + 2] *= r.z;
-          st.o[mt][4 * q + 3] *= r.w;
-        }
+      // a new chunk (c_prev == c - 1: every chunk has a block): its logit bias from the piece's LDS table (O is in
+      // true V units, so it carries over unchanged)
       beta = bias_tab[c * QT];
       tk = beta - m_ref + (P_OFFSET - RESCALE_SLACK);
       c_prev = c;
@@ -582,51 +580,43 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   phase_barrier();               // every wave is done with the stages before they are refilled
   st.m = m_ref;
   st.l = halves_sum(l_run);
-  st.c_last = c_prev;
 }
 
-// Whole tile: O = o * v_scale / l as bf16; lane (query lq) writes channels 32 mt + 8 i + 4 g + (0..3).
-__device__ __forceinline__ void store_out(const AttnArgs& a, const Piece& st, const float* __restrict__ v_scale,
-                                          uint16_t* __restrict__ out, int bh, int64_t q0) {
+// Whole tile: O = o / l as bf16; lane (query lq) writes channels 32 mt + 8 i + 4 g + (0..3).
+__device__ __forceinline__ void store_out(const AttnArgs& a, const Piece& st, uint16_t* __restrict__ out, int bh,
+                                          int64_t q0) {
   const int lane = threadIdx.x & 63, lq = lane & 31, g = lane >> 5;
   const int64_t qrow = q0 + lq;
   if (qrow >= a.lq) return;
   const float inv_l = 1.f / st.l;
   const int64_t b = bh / a.heads, h = bh % a.heads;
   uint16_t* op = out + b * a.o_sb + qrow * a.o_st + h * a.o_sh;
-  const float* vs = v_scale + ((int64_t)a.seg_slot[st.c_last] * a.bh + bh) * D;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ch = 32 * mt + 8 * i + 4 * g;
-      const uint32_t w0 = f32_to_bf16_bits(st.o[mt][4 * i] * vs[ch] * inv_l) |
-                          ((uint32_t)f32_to_bf16_bits(st.o[mt][4 * i + 1] * vs[ch + 1] * inv_l) << 16);
-      const uint32_t w1 = f32_to_bf16_bits(st.o[mt][4 * i + 2] * vs[ch + 2] * inv_l) |
-                          ((uint32_t)f32_to_bf16_bits(st.o[mt][4 * i + 3] * vs[ch + 3] * inv_l) << 16);
+      const uint32_t w0 = f32_to_bf16_bits(st.o[mt][4 * i] * inv_l) |
+                          ((uint32_t)f32_to_bf16_bits(st.o[mt][4 * i + 1] * inv_l) << 16);
+      const uint32_t w1 = f32_to_bf16_bits(st.o[mt][4 * i + 2] * inv_l) |
+                          ((uint32_t)f32_to_bf16_bits(st.o[mt][4 * i + 3] * inv_l) << 16);
       *(uint2*)(op + ch) = make_uint2(w0, w1);
     }
 }
 
-// Part of a tile: o * v_scale (unnormalised) and (m, l) per row into workspace slot (g, slot).
-__device__ __forceinline__ void store_part(const AttnArgs& a, const Piece& st, const float* __restrict__ v_scale,
-                                           float* __restrict__ o_part, float* __restrict__ ml_part, int bh,
+// Part of a tile: o (unnormalised) and (m, l) per row into workspace slot (g, slot).
+__device__ __forceinline__ void store_part(const Piece& st, float* __restrict__ o_part, float* __restrict__ ml_part,
                                            int64_t slot_idx, int w) {
   const int lane = threadIdx.x & 63, lq = lane & 31, g = lane >> 5;
   const int row = w * 32 + lq;
   float* op = o_part + (slot_idx * QT + row) * D;
-  const float* vs = v_scale + ((int64_t)a.seg_slot[st.c_last] * a.bh + bh) * D;
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ch = 32 * mt + 8 * i + 4 * g;
-      float4 v;
-      v.x = st.o[mt][4 * i] * vs[ch];
-      v.y = st.o[mt][4 * i + 1] * vs[ch + 1];
-      v.z = st.o[mt][4 * i + 2] * vs[ch + 2];
-      v.w = st.o[mt][4 * i + 3] * vs[ch + 3];
-      *(float4*)(op + ch) = v;
+      *(float4*)(op + ch) = make_float4(st.o[mt][4 * i], st.o[mt][4 * i + 1], st.o[mt][4 * i + 2],
+                                        st.o[mt][4 * i + 3]);
     }
   if (g == 0) *(float2*)(ml_part + (slot_idx * QT + row) * 2) = make_float2(st.m, st.l);
 }
@@ -639,7 +629,7 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* _
                                                                  const float* __restrict__ k_scale,
                                                                  const uint8_t* __restrict__ v8,
                                                                  const uint8_t* __restrict__ v8lo,
-                                                                 const float* __restrict__ v_scale,
+                                                                 const uint8_t* __restrict__ v_scale,
                                                                  uint16_t* __restrict__ out, float* __restrict__ o_part,
                                                                  float* __restrict__ ml_part, int32_t* __restrict__ logits,
                                                                  AttnArgs a) {
@@ -653,7 +643,7 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* _
     const int bh = tile / a.q_tiles;
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
     attend_range<TWO, LOGITS>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, 0, a.nb, st, logits);
-    store_out(a, st, v_scale, out, bh, q0);
+    store_out(a, st, out, bh, q0);
   }
   // this workgroup's piece of the split tiles
   if (p.units == 0) return;
@@ -667,9 +657,9 @@ __global__ __launch_bounds__(AT_THREADS, 1) void attn_fwd_kernel(const int8_t* _
     const int64_t q0 = (int64_t)(tile % a.q_tiles) * QT + w * 32;
     attend_range<TWO, LOGITS>(a, q8, q_scale, bias, k8, k_scale, v8, v8lo, v_scale, lds, bh, q0, j0, j1, st, logits);
     if (j0 == 0 && j1 == a.nb) {
-      store_out(a, st, v_scale, out, bh, q0);
+      store_out(a, st, out, bh, q0);
     } else {
-      store_part(a, st, v_scale, o_part, ml_part, bh, (int64_t)gid * 2 + (tile == first_tile ? 0 : 1), w);
+      store_part(st, o_part, ml_part, (int64_t)gid * 2 + (tile == first_tile ? 0 : 1), w);
     }
     u += j1 - j0;
   }
@@ -790,7 +780,7 @@ extern "C" int64_t lbw_attn_workspace_bytes(void) {
 // every block's raw QK^T accumulator words there.
 static int attn_launch(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch, int64_t lq,
                        int64_t heads, const int8_t* k8, const float* k_scale, const uint8_t* v8, const uint8_t* v8lo,
-                       const float* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
+                       const uint8_t* v_scale, int64_t slots, int64_t cap, int n_seg, const int32_t* seg_slot,
                        const int32_t* seg_len, const int32_t* seg_first, uint16_t* out, int64_t o_s_batch,
                        int64_t o_s_tok, int64_t o_s_head, float sm_scale, int32_t* logits, void* workspace,
                        void* stream) {
@@ -802,7 +792,7 @@ static int attn_launch(const int8_t* q8, const float* q_scale, const float* bias
   if (n_seg > 1 && !bias) return LBW_E_NULL;
   if (o_s_batch % 4 || o_s_tok % 4 || o_s_head % 4) return LBW_E_ALIGN;
   if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo | (uintptr_t)workspace) & 15 ||
-      ((uintptr_t)out & 7) || ((uintptr_t)logits & 3))
+      ((uintptr_t)out & 7) || (((uintptr_t)logits | (uintptr_t)v_scale) & 3))
     return LBW_E_ALIGN;
   AttnArgs a;
   a.lq = lq;
@@ -865,7 +855,7 @@ static int attn_launch(const int8_t* q8, const float* q_scale, const float* bias
 
 extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
                             int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
-                            const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
+                            const uint8_t* v8, const uint8_t* v8lo, const uint8_t* v_scale, int64_t slots,
                             int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
                             const int32_t* seg_first, uint16_t* out, int64_t o_s_batch, int64_t o_s_tok,
                             int64_t o_s_head, float sm_scale, void* workspace, void* stream) {
@@ -875,7 +865,7 @@ extern "C" int lbw_attn_fwd(const int8_t* q8, const float* q_scale, const float*
 
 extern "C" int lbw_qk_logits_i32(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
                                  int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
-                                 const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
+                                 const uint8_t* v8, const uint8_t* v8lo, const uint8_t* v_scale, int64_t slots,
                                  int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
                                  const int32_t* seg_first, uint16_t* out, int64_t o_s_batch, int64_t o_s_tok,
                                  int64_t o_s_head, float sm_scale, int32_t* logits, void* workspace, void* stream) {
@@ -911,7 +901,7 @@ extern "C" int64_t lbw_attn_noalloc_scratch_bytes(void) { return ATTN_SCRATCH_BY
 
 extern "C" int lbw_attn_fwd_noalloc(const int8_t* q8, const float* q_scale, const float* bias, int64_t batch,
                                     int64_t lq, int64_t heads, const int8_t* k8, const float* k_scale,
-                                    const uint8_t* v8, const uint8_t* v8lo, const float* v_scale, int64_t slots,
+                                    const uint8_t* v8, const uint8_t* v8lo, const uint8_t* v_scale, int64_t slots,
                                     int64_t cap, int n_seg, const int32_t* seg_slot, const int32_t* seg_len,
                                     const int32_t* seg_first, uint16_t* out, int64_t o_s_batch, int64_t o_s_tok,
                                     int64_t o_s_head, float sm_scale, void* stream) {

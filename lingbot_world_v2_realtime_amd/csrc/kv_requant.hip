@@ -1,19 +1,25 @@
 // K/V re-quant of finished chunks into the quantised ring cache (gfx950).
 //
 // Three launches:
-//   1. kv_stats:    per 64-token block (grid: block, batch*head, layer), fp32 column sums of K and column max |V|
-//                   of each 32-token half (K and V read once, with non-temporal loads: -12 % for 30 layers).
-//   2. kv_finalize: per (batch*head, layer, 16 channels), the half-block partials summed into blocks and 4-block
-//                   super-blocks in parallel, the super-blocks left to right, then the mean -> bf16, the V scale (the power of
-//                   two 2^e with amax / 2^e in (224, 448]) and its reciprocal.
-//   3. kv_quant:    K - mean -> int8 per 64-token block; y = V * 2^-e (exact) -> e4m3 hi = rn(y) and, when a
-//                   second plane is given, lo = rn((y - hi) * 16), both in the permuted block layout (reads K and
-//                   V a second time).
+//   1. kv_stats:    per 64-token block (grid: block, batch*head, layer): fp32 column sums of K for each 32-token
+//                   half, and all of V's quantisation -- V is read once. A block's V scales are powers of two, one per
+//                   (key group, channel): group g is the block's 32-token half g, the K-block g of the attention's
+//                   64-deep fp8 PV MFMA, whose per-lane E8M0 block scale then applies the scale. 2^e takes the
+//                   group's amax into (224, 448]; y = V * 2^-e (exact) -> e4m3
+//                   hi = rn(y) and, when a second plane is given, lo = rn((y - hi) * 16), both in the permuted block
+//                   layout, and the block's 256-byte E8M0 table (byte (32 g + c % 32) * 4 + c / 32 = 127 + e of
+//                   channel c, group g: the attention lane that scales channel c's row for group g reads dword
+//                   32 g + c % 32 and selects byte c / 32).
+//   2. kv_finalize: per (batch*head, layer, 16 channels), the half-block sums added into blocks and 4-block
+//                   super-blocks in parallel, the super-blocks left to right, then the mean in the inputs' format.
+//   3. kv_quant:    K - mean -> int8 per 64-token block (reads K a second time); with V (a caller that wrote the
+//                   K partials itself and never read V) also V as in pass 1.
 // The column-sum order is fixed (see the oracle's chunk_mean): s = x[4q] + x[4q+1] + x[4q+2] + x[4q+3] per
 // thread, q = 0..7 and q = 8..15 left to right per half-block, the two halves added, the blocks of each 4-block
 // super-block left to right, then the super-blocks left to right, so the mean is the same bits on every run and
 // on the CPU. (The halves let a producer that sees 32 tokens at a time write the partials itself.)
 #include <algorithm>
+#include <type_traits>
 
 #include "lbw_common.h"
 
@@ -28,23 +34,121 @@ struct ReqArgs {
 constexpr int REQ_SUPER = 4;   // blocks per super-block of the mean's defined order
 constexpr int FIN_U = 8;       // super-block sums per lane the finaliser holds in LDS at a time
 
-// Thread (cg, q) = (t & 15, t >> 4) sums channels 8 cg .. + 8 over tokens 4 q .. 4 q + 3 of the block. F16: the
-// inputs are fp16 (else bf16).
+// V of one 64-token block, quantised by the block's 256 threads. Thread t = (cg, kq) = (t & 15, t >> 4) holds
+// channels 8 cg .. + 8 of keys 4 kq .. 4 kq + 3, all of group kq >> 3 (waves 0-1: group 0, waves 2-3: group 1), so
+// its e4m3 bytes of one channel are 4 adjacent positions (one dword) of the permuted layout. Steps separated by
+// workgroup barriers.
+struct VBlockLds {
+  uint32_t tile[2][D * 16];   // hi / lo planes: [channel][16 dwords], dword xor-swizzled by channel >> 3
+  float gmax[4][D];           // per wave: max |V| of each channel over the wave's 16 keys
+  float rec[2][D];            // 2^-e of [group][channel]
+};
+
+// Step 1: the thread's 4 x 8 values, and the wave's per-group column maxima into LDS.
+template <bool F16>
+__device__ __forceinline__ void vblock_max(const v4i* vw, float (&vf)[4][8], VBlockLds& s) {
+  const int t = threadIdx.x, lane = t & 63, cg = t & 15;
+  float m[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) m[c] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    unpack8t<F16>(vw[j], vf[j]);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) m[c] = fmaxf(m[c], fabsf(vf[j][c]));
+  }
+  // the wave's four key quads of these channels: lanes cg + 16 i
+#pragma unroll
+  for (int c = 0; c < 8; ++c) m[c] = max_xor32(max_xor16(m[c]));
+  if (lane < 16) {
+    float* gm = &s.gmax[t >> 6][cg * 8];
+    *(float4*)gm = make_float4(m[0], m[1], m[2], m[3]);
+    *(float4*)(gm + 4) = make_float4(m[4], m[5], m[6], m[7]);
+  }
+}
+
+// Step 2: thread t forms the scale of table byte t (group t >> 7, channel 32 (t & 3) + ((t >> 2) & 31)): the
+// power of two 2^e with amax / 2^e in (224, 448]. amax = f * 2^x with f in [0.5, 1) (a normal float after the
+// floor): e = x - 9 when f <= 0.875 (mantissa bits <= 0x600000), else x - 8; x = biased exponent - 126.
+__device__ __forceinline__ void vblock_scale(VBlockLds& s, uint8_t* __restrict__ table) {
+  const int t = threadIdx.x, g = t >> 7, ch = 32 * (t & 3) + ((t >> 2) & 31);
+  float mx = fmaxf(s.gmax[2 * g][ch], s.gmax[2 * g + 1][ch]);   // the group's two waves
+  mx = fmaxf(mx, AMAX_FLOOR);
+  const uint32_t mb = __float_as_uint(mx);
+  const int e = (int)(mb >> 23) - ((mb & 0x7FFFFFu) <= 0x600000u ? 135 : 134);
+  s.rec[g][ch] = __uint_as_float((uint32_t)(127 - e) << 23);
+  table[t] = (uint8_t)(127 + e);
+}
+
+// Step 3: e4m3 bytes into the transposed LDS tile.
+__device__ __forceinline__ void vblock_quant(const float (&vf)[4][8], bool two, VBlockLds& s) {
+  const int t = threadIdx.x, cg = t & 15, kq = t >> 4;
+  float rec[8];
+  {
+    const float* rp = &s.rec[kq >> 3][cg * 8];
+    const float4 r0 = *(const float4*)rp, r1 = *(const float4*)(rp + 4);
+    rec[0] = r0.x; rec[1] = r0.y; rec[2] = r0.z; rec[3] = r0.w;
+    rec[4] = r1.x; rec[5] = r1.y; rec[6] = r1.z; rec[7] = r1.w;
+  }
+  uint32_t vb[8], vl[8];   // per channel: 4 e4m3 bytes (hi, lo) of keys 4kq .. 4kq+3
+#pragma unroll
+  for (int c = 0; c < 8; ++c) { vb[c] = 0; vl[c] = 0; }
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int c = 0; c < 8; c += 2) {
+      // |V| * 2^-e <= 448 by the choice of e, and the product is exact (a power-of-two factor)
+      const float y0 = fminf(fmaxf(__fmul_rn(vf[j][c], rec[c]), -V_MAX), V_MAX);
+      const float y1 = fminf(fmaxf(__fmul_rn(vf[j][c + 1], rec[c + 1]), -V_MAX), V_MAX);
+      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+      vb[c] |= ((uint32_t)pk & 0xFFu) << (8 * j);
+      vb[c + 1] |= (((uint32_t)pk >> 8) & 0xFFu) << (8 * j);
+      if (two) {   // residual plane: (y - hi) * 16 is exact in fp32 and within the e4m3 range
+        const float r0 = __fmul_rn(__fsub_rn(y0, __builtin_amdgcn_cvt_f32_fp8(pk, 0)), V_LO_SCALE);
+        const float r1 = __fmul_rn(__fsub_rn(y1, __builtin_amdgcn_cvt_f32_fp8(pk, 1)), V_LO_SCALE);
+        const uint32_t pl = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false);
+        vl[c] |= (pl & 0xFFu) << (8 * j);
+        vl[c + 1] |= ((pl >> 8) & 0xFFu) << (8 * j);
+      }
+    }
+  // row = channel, dword = position / 4
+  const int pdw = v_pos_of_key(kq * 4) >> 2;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int ch = cg * 8 + c;
+    s.tile[0][ch * 16 + (pdw ^ (ch >> 3))] = vb[c];
+    if (two) s.tile[1][ch * 16 + (pdw ^ (ch >> 3))] = vl[c];
+  }
+}
+
+// Step 4: the tiles out; thread t writes 32 contiguous bytes (channel t >> 1, positions 32 * (t & 1) ..) of each plane.
+__device__ __forceinline__ void vblock_store(const VBlockLds& s, uint8_t* __restrict__ v8, uint8_t* __restrict__ v8lo,
+                                             int64_t tile) {
+  const int t = threadIdx.x, ch = t >> 1, d0 = (t & 1) * 8;
+  for (int pl = 0; pl < (v8lo ? 2 : 1); ++pl) {
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = s.tile[pl][ch * 16 + ((d0 + i) ^ (ch >> 3))];
+    uint8_t* vout = (pl ? v8lo : v8) + tile * (D * KB) + ch * KB + d0 * 4;
+    store_once(vout, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
+    store_once(vout + 16, v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]});
+  }
+}
+
+// Thread (cg, q) = (t & 15, t >> 4) sums channels 8 cg .. + 8 over tokens 4 q .. 4 q + 3 of the block and holds the
+// same channels and tokens of V. F16: the inputs are fp16 (else bf16).
 template <bool F16>
 __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, ReqArgs a,
-                                                       float* __restrict__ part_sum,
-                                                       float* __restrict__ part_amax) {
+                                                       float* __restrict__ part_sum, uint8_t* __restrict__ v8,
+                                                       uint8_t* __restrict__ v8lo, uint8_t* __restrict__ v_scale) {
   __shared__ float s_sum[16][D];
-  __shared__ float s_max[16][D];
+  __shared__ VBlockLds s_v;
   const int blk = blockIdx.x, bh = blockIdx.y, layer = blockIdx.z;
   const int t = threadIdx.x, cg = t & 15, q = t >> 4;
   const int64_t b = bh / a.heads, h = bh % a.heads;
   const uint16_t* kp = k + layer * a.k_sl + b * a.k_sb + h * a.k_sh + cg * 8;
   const uint16_t* vp = v + layer * a.v_sl + b * a.v_sb + h * a.v_sh + cg * 8;
-  float s[8], m[8];
-#pragma unroll
-  for (int c = 0; c < 8; ++c) { s[c] = 0.f; m[c] = 0.f; }
   v4i kw[4], vw[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -53,56 +157,51 @@ __global__ __launch_bounds__(256) void kv_stats_kernel(const uint16_t* __restric
     kw[j] = ok ? load_once(kp + tok * a.k_st) : v4i{0, 0, 0, 0};
     vw[j] = ok ? load_once(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
   }
+  float s[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) s[c] = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    float kf[8], vf[8];
+    float kf[8];
     unpack8t<F16>(kw[j], kf);
-    unpack8t<F16>(vw[j], vf);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      s[c] = __fadd_rn(s[c], kf[c]);
-      m[c] = fmaxf(m[c], fabsf(vf[c]));
-    }
+    for (int c = 0; c < 8; ++c) s[c] = __fadd_rn(s[c], kf[c]);
   }
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    s_sum[q][cg * 8 + c] = s[c];
-    s_max[q][cg * 8 + c] = m[c];
-  }
+  for (int c = 0; c < 8; ++c) s_sum[q][cg * 8 + c] = s[c];
+  float vf[4][8];
+  vblock_max<F16>(vw, vf, s_v);
   __syncthreads();
   {   // thread t: half t >> 7 of the block, channel t & 127
     const int c = t & (D - 1), r0 = (t >> 7) * 8;
-    float acc = 0.f, mx = 0.f;
+    float acc = 0.f;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      acc = __fadd_rn(acc, s_sum[r0 + r][c]);
-      mx = fmaxf(mx, s_max[r0 + r][c]);
-    }
-    const int64_t o = ((((int64_t)layer * a.bh + bh) * a.nb + blk) * 2 + (t >> 7)) * D + c;
-    part_sum[o] = acc;
-    part_amax[o] = mx;
+    for (int r = 0; r < 8; ++r) acc = __fadd_rn(acc, s_sum[r0 + r][c]);
+    part_sum[((((int64_t)layer * a.bh + bh) * a.nb + blk) * 2 + (t >> 7)) * D + c] = acc;
   }
+  const int64_t tile = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * a.nbc + blk;
+  vblock_scale(s_v, v_scale + tile * 256);
+  __syncthreads();
+  vblock_quant(vf, v8lo != nullptr, s_v);
+  __syncthreads();
+  vblock_store(s_v, v8, v8lo, tile);
 }
 
 // One workgroup per (batch*head, layer, group of 16 channels). Thread (j, c) = (t >> 4, t & 15) forms the
 // super-block sums U[u] = B[4u] + .. + B[4u+3] of channel 16 cgrp + c for u = j, j + 16, .. (all of them at
-// once, in parallel), and the maxima; then one thread per channel sums the U left to right.
+// once, in parallel); then one thread per channel sums the U left to right.
 constexpr int FIN_CH = 16;                 // channels per finaliser workgroup
 constexpr int FIN_J = 256 / FIN_CH;        // super-block lanes per channel
 template <bool F16>
 __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float* __restrict__ part_sum,
-                                                          const float* __restrict__ part_amax,
-                                                          float* __restrict__ v_recip, float* __restrict__ km,
-                                                          float* __restrict__ v_scale) {
+                                                          float* __restrict__ km) {
   __shared__ float buf[FIN_U * FIN_J * FIN_CH];
-  __shared__ float s_mx[FIN_J][FIN_CH];
   const int bh = blockIdx.x, layer = blockIdx.y, cgrp = blockIdx.z;
   const int t = threadIdx.x, c = t & (FIN_CH - 1), j = t / FIN_CH, ch = cgrp * FIN_CH + c;
   const int64_t grp = (int64_t)layer * a.bh + bh;
   const float* bsum = part_sum + grp * a.nb * 2 * D + ch;   // [block][half][channel]
-  const float* bmax = part_amax + grp * a.nb * 2 * D + ch;
   const int nsup = (int)((a.nb + REQ_SUPER - 1) / REQ_SUPER);
-  float tot = 0.f, mx = 0.f;
+  float tot = 0.f;
   for (int u0 = 0; u0 < nsup; u0 += FIN_U * FIN_J) {
     const int nu = min(FIN_U * FIN_J, nsup - u0);
     for (int uu = j; uu < nu; uu += FIN_J) {
@@ -113,7 +212,6 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
         const bool ok = b0 + i < a.nb;
         const int64_t o = (int64_t)(b0 + i) * 2 * D;
         us = __fadd_rn(us, ok ? __fadd_rn(bsum[o], bsum[o + D]) : 0.f);
-        mx = fmaxf(mx, ok ? fmaxf(bmax[o], bmax[o + D]) : 0.f);
       }
       buf[uu * FIN_CH + c] = us;
     }
@@ -122,99 +220,70 @@ __global__ __launch_bounds__(256) void kv_finalize_kernel(ReqArgs a, const float
       for (int uu = 0; uu < nu; ++uu) tot = __fadd_rn(tot, buf[uu * FIN_CH + c]);
     __syncthreads();
   }
-  s_mx[j][c] = mx;
-  __syncthreads();
   if (j == 0) {
-#pragma unroll
-    for (int jj = 1; jj < FIN_J; ++jj) mx = fmaxf(mx, s_mx[jj][c]);
-    mx = fmaxf(mx, AMAX_FLOOR);
     const int64_t so = (((int64_t)layer * a.slots + a.slot) * a.bh + bh) * D + ch;
     km[so] = round16<F16>(__fdiv_rn(tot, (float)a.len));   // the mean in the inputs' own format
-    // amax = f * 2^x with f in [0.5, 1) (mx is a normal float): 2^e takes it into (224, 448] = (0.875 * 2^8,
-    // 0.875 * 2^9] with e = x - 9 when f <= 0.875 (mantissa bits <= 0x600000), else x - 8; x = biased exponent - 126
-    const uint32_t mb = __float_as_uint(mx);
-    const int e = (int)(mb >> 23) - ((mb & 0x7FFFFFu) <= 0x600000u ? 135 : 134);
-    v_scale[so] = __uint_as_float((uint32_t)(127 + e) << 23);
-    v_recip[grp * D + ch] = __uint_as_float((uint32_t)(127 - e) << 23);
   }
 }
 
-// Thread t owns channels 8*(t & 15) .. +8 and the 4 consecutive keys 4*(t >> 4) .. +4 of the block, so its
-// e4m3 V bytes for one channel are 4 adjacent positions (one dword) of the permuted layout. Layers go last to
-// first: the statistics pass read the last layers most recently, so the first re-reads can still find them in
-// the memory-side cache.
-template <bool F16>
+// Thread t owns channels 8*(t & 15) .. +8 and the 4 consecutive keys 4*(t >> 4) .. +4 of the block. Layers go last
+// to first: the statistics pass read the last layers most recently, so the first re-reads can still find them in
+// the memory-side cache. WITH_V: V of the block is quantised here too.
+template <bool F16, bool WITH_V>
 __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restrict__ k,
                                                        const uint16_t* __restrict__ v, ReqArgs a,
-                                                       const float* __restrict__ v_recip,
                                                        int8_t* __restrict__ k8, float* __restrict__ k_scale,
-                                                       const float* __restrict__ km,
-                                                       uint8_t* __restrict__ v8, uint8_t* __restrict__ v8lo) {
-  __shared__ uint32_t s_v[2][D * 16];   // hi / lo planes: [channel][16 dwords], dword xor-swizzled by channel >> 3
+                                                       const float* __restrict__ km, uint8_t* __restrict__ v8,
+                                                       uint8_t* __restrict__ v8lo, uint8_t* __restrict__ v_scale) {
   __shared__ float s_red[4];
+  __shared__ std::conditional_t<WITH_V, VBlockLds, int> s_v;   // (no V tile without V)
   const int blk = blockIdx.x, bh = blockIdx.y, layer = gridDim.z - 1 - blockIdx.z;
   const int t = threadIdx.x, cg = t & 15, kq = t >> 4;
   const int64_t b = bh / a.heads, h = bh % a.heads;
   const uint16_t* kp = k + layer * a.k_sl + b * a.k_sb + h * a.k_sh + cg * 8;
-  const uint16_t* vp = v + layer * a.v_sl + b * a.v_sb + h * a.v_sh + cg * 8;
   const int64_t slot_bh = ((int64_t)layer * a.slots + a.slot) * a.bh + bh;
-  float mean[8], vrec[8];
+  float mean[8];
   {
     const float* kmp = km + slot_bh * D + cg * 8;
-    const float* vrp = v_recip + ((int64_t)layer * a.bh + bh) * D + cg * 8;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) { mean[c] = kmp[c]; vrec[c] = vrp[c]; }
+    for (int c = 0; c < 8; ++c) mean[c] = kmp[c];
+  }
+  v4i vw[4];
+  if constexpr (WITH_V) {
+    const uint16_t* vp = v + layer * a.v_sl + b * a.v_sb + h * a.v_sh + cg * 8;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t tok = (int64_t)blk * KB + kq * 4 + j;
+      vw[j] = tok < a.len ? *(const v4i*)(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
+    }
   }
   float x[4][8];
-  uint32_t vb[8], vl[8];   // per channel: 4 e4m3 bytes (hi, lo) of keys 4kq .. 4kq+3
-#pragma unroll
-  for (int c = 0; c < 8; ++c) { vb[c] = 0; vl[c] = 0; }
   float amax = 0.f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t tok = (int64_t)blk * KB + kq * 4 + j;
     const bool ok = tok < a.len;
     v4i kw = ok ? *(const v4i*)(kp + tok * a.k_st) : v4i{0, 0, 0, 0};
-    v4i vw = ok ? *(const v4i*)(vp + tok * a.v_st) : v4i{0, 0, 0, 0};
-    float kf[8], vf[8];
+    float kf[8];
     unpack8t<F16>(kw, kf);
-    unpack8t<F16>(vw, vf);
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       x[j][c] = ok ? __fsub_rn(kf[c], mean[c]) : 0.f;
       amax = fmaxf(amax, fabsf(x[j][c]));
     }
-#pragma unroll
-    for (int c = 0; c < 8; c += 2) {
-      float y0 = fminf(fmaxf(__fmul_rn(vf[c], vrec[c]), -V_MAX), V_MAX);
-      float y1 = fminf(fmaxf(__fmul_rn(vf[c + 1], vrec[c + 1]), -V_MAX), V_MAX);
-      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-      vb[c] |= ((uint32_t)pk & 0xFFu) << (8 * j);
-      vb[c + 1] |= (((uint32_t)pk >> 8) & 0xFFu) << (8 * j);
-      // residual plane: (y - hi) * 16 is exact in fp32 and within the e4m3 range
-      const float r0 = __fmul_rn(__fsub_rn(y0, __builtin_amdgcn_cvt_f32_fp8(pk, 0)), V_LO_SCALE);
-      const float r1 = __fmul_rn(__fsub_rn(y1, __builtin_amdgcn_cvt_f32_fp8(pk, 1)), V_LO_SCALE);
-      const uint32_t pl = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false);
-      vl[c] |= (pl & 0xFFu) << (8 * j);
-      vl[c + 1] |= ((pl >> 8) & 0xFFu) << (8 * j);
-    }
   }
   // block amax over 64 tokens x 128 channels
   amax = wave_max(amax);
   if ((t & 63) == 0) s_red[t >> 6] = amax;
-  // e4m3 V dwords into the transposed tile: row = channel, dword = position / 4
-  const int pdw = v_pos_of_key(kq * 4) >> 2;
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const int ch = cg * 8 + c;
-    s_v[0][ch * 16 + (pdw ^ (ch >> 3))] = vb[c];
-    s_v[1][ch * 16 + (pdw ^ (ch >> 3))] = vl[c];
-  }
+  float vf[4][8];
+  if constexpr (WITH_V) vblock_max<F16>(vw, vf, s_v);
   __syncthreads();
+  const int64_t tile = slot_bh * a.nbc + blk;
+  if constexpr (WITH_V) vblock_scale(s_v, v_scale + tile * 256);
   amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   amax = fmaxf(amax, AMAX_FLOOR);
   const float recip = __fdiv_rn(127.f, amax);
-  if (t == 0) k_scale[slot_bh * a.nbc + blk] = __fdiv_rn(amax, 127.f);
+  if (t == 0) k_scale[tile] = __fdiv_rn(amax, 127.f);
   int8_t* kout = k8 + (slot_bh * a.cap + (int64_t)blk * KB) * D + cg * 8;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -226,33 +295,29 @@ __global__ __launch_bounds__(256) void kv_quant_kernel(const uint16_t* __restric
     }
     store_once(kout + (kq * 4 + j) * D, v2i{(int)lo, (int)hi});
   }
-  // V tiles out: thread t writes 32 contiguous bytes (channel t >> 1, positions 32 * (t & 1) ..) of each plane
-  for (int pl = 0; pl < (v8lo ? 2 : 1); ++pl) {
-    const int ch = t >> 1, d0 = (t & 1) * 8;
-    uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = s_v[pl][ch * 16 + ((d0 + i) ^ (ch >> 3))];
-    uint8_t* vout = (pl ? v8lo : v8) + (slot_bh * a.nbc + blk) * (D * KB) + ch * KB + d0 * 4;
-    store_once(vout, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
-    store_once(vout + 16, v4i{(int)w[4], (int)w[5], (int)w[6], (int)w[7]});
+  if constexpr (WITH_V) {
+    __syncthreads();
+    vblock_quant(vf, v8lo != nullptr, s_v);
+    __syncthreads();
+    vblock_store(s_v, v8, v8lo, tile);
   }
 }
 
 int kv_requant_check(int64_t layers, int64_t batch, int64_t len, int64_t heads, const int8_t* k8,
                      const float* k_scale, const float* km, const uint8_t* v8, const uint8_t* v8lo,
-                     const float* v_scale, int64_t slots, int64_t cap, int64_t slot) {
+                     const uint8_t* v_scale, int64_t slots, int64_t cap, int64_t slot) {
   if (!k8 || !k_scale || !km || !v8 || !v_scale) return LBW_E_NULL;
   if (layers <= 0 || batch <= 0 || heads <= 0 || len <= 0 || slots <= 0 || cap <= 0) return LBW_E_SHAPE;
   if (cap % KB != 0 || len > cap || slot < 0 || slot >= slots) return LBW_E_SHAPE;
   if (layers > 65535 || batch * heads > 65535 || cap / KB > (int64_t)1 << 30) return LBW_E_SHAPE;
-  if (((uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo) & 15) return LBW_E_ALIGN;
+  if (((uintptr_t)k8 | (uintptr_t)v8 | (uintptr_t)v8lo) & 15 || (uintptr_t)v_scale & 3) return LBW_E_ALIGN;
   return LBW_OK;
 }
 
 int kv_requant_launch(bool with_stats, bool f16, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
                       int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok,
                       int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
-                      int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,
+                      int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, uint8_t* v_scale,
                       int64_t slots, int64_t cap, int64_t slot, void* workspace, void* stream) {
   if (!k || !v || !workspace) return LBW_E_NULL;
   if (const int st = kv_requant_check(layers, batch, len, heads, k8, k_scale, km, v8, v8lo, v_scale, slots, cap,
@@ -269,22 +334,31 @@ int kv_requant_launch(bool with_stats, bool f16, const uint16_t* k, const uint16
   a.k_sl = k_s_layer; a.k_sb = k_s_batch; a.k_st = k_s_tok; a.k_sh = k_s_head;
   a.v_sl = v_s_layer; a.v_sb = v_s_batch; a.v_st = v_s_tok; a.v_sh = v_s_head;
   float* part_sum = (float*)workspace;
-  float* part_amax = part_sum + layers * a.bh * a.nb * 2 * D;
-  float* v_recip = part_amax + layers * a.bh * a.nb * 2 * D;
   if (const int dv = check_device()) return dv;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)a.nb, (unsigned)a.bh, (unsigned)layers);
   const dim3 fgrid((unsigned)a.bh, (unsigned)layers, D / FIN_CH);
+  // with the statistics pass, V is quantised there and the last pass is K only; without it, the last pass does both
   if (f16) {
-    if (with_stats) hipLaunchKernelGGL(kv_stats_kernel<true>, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
-    hipLaunchKernelGGL(kv_finalize_kernel<true>, fgrid, dim3(256), 0, st, a, part_sum, part_amax, v_recip, km,
-                       v_scale);
-    hipLaunchKernelGGL(kv_quant_kernel<true>, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
+    if (with_stats)
+      hipLaunchKernelGGL(kv_stats_kernel<true>, grid, dim3(256), 0, st, k, v, a, part_sum, v8, v8lo, v_scale);
+    hipLaunchKernelGGL(kv_finalize_kernel<true>, fgrid, dim3(256), 0, st, a, part_sum, km);
+    if (with_stats)
+      hipLaunchKernelGGL((kv_quant_kernel<true, false>), grid, dim3(256), 0, st, k, v, a, k8, k_scale, km, v8, v8lo,
+                         v_scale);
+    else
+      hipLaunchKernelGGL((kv_quant_kernel<true, true>), grid, dim3(256), 0, st, k, v, a, k8, k_scale, km, v8, v8lo,
+                         v_scale);
   } else {
-    if (with_stats) hipLaunchKernelGGL(kv_stats_kernel<false>, grid, dim3(256), 0, st, k, v, a, part_sum, part_amax);
-    hipLaunchKernelGGL(kv_finalize_kernel<false>, fgrid, dim3(256), 0, st, a, part_sum, part_amax, v_recip, km,
-                       v_scale);
-    hipLaunchKernelGGL(kv_quant_kernel<false>, grid, dim3(256), 0, st, k, v, a, v_recip, k8, k_scale, km, v8, v8lo);
+    if (with_stats)
+      hipLaunchKernelGGL(kv_stats_kernel<false>, grid, dim3(256), 0, st, k, v, a, part_sum, v8, v8lo, v_scale);
+    hipLaunchKernelGGL(kv_finalize_kernel<false>, fgrid, dim3(256), 0, st, a, part_sum, km);
+    if (with_stats)
+      hipLaunchKernelGGL((kv_quant_kernel<false, false>), grid, dim3(256), 0, st, k, v, a, k8, k_scale, km, v8, v8lo,
+                         v_scale);
+    else
+      hipLaunchKernelGGL((kv_quant_kernel<false, true>), grid, dim3(256), 0, st, k, v, a, k8, k_scale, km, v8, v8lo,
+                         v_scale);
   }
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
@@ -297,14 +371,14 @@ using namespace lbw;
 extern "C" int64_t lbw_kv_requant_workspace_bytes(int64_t layers, int64_t bh, int64_t len) {
   if (layers <= 0 || bh <= 0 || len <= 0) return 0;
   const int64_t nb = (len + KB - 1) / KB;
-  return (4 * layers * bh * nb * D + layers * bh * D) * (int64_t)sizeof(float);
+  return 2 * layers * bh * nb * D * (int64_t)sizeof(float);
 }
 
 extern "C" int lbw_kv_requant(const uint16_t* k, const uint16_t* v, int dtype, int64_t layers, int64_t batch,
                               int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch,
                               int64_t k_s_tok, int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch,
                               int64_t v_s_tok, int64_t v_s_head, int8_t* k8, float* k_scale, float* km,
-                              uint8_t* v8, uint8_t* v8lo, float* v_scale, int64_t slots, int64_t cap,
+                              uint8_t* v8, uint8_t* v8lo, uint8_t* v_scale, int64_t slots, int64_t cap,
                               int64_t slot, void* workspace, void* stream) {
   if (dtype != LBW_DTYPE_BF16 && dtype != LBW_DTYPE_FP16) return LBW_E_SHAPE;
   return kv_requant_launch(true, dtype == LBW_DTYPE_FP16, k, v, layers, batch, len, heads, k_s_layer, k_s_batch,

@@ -157,15 +157,16 @@ __device__ __forceinline__ float wave_max(float x) {
 int check_device();
 
 // The K/V re-quant's argument checks of the ring side, and its launches (kv_requant.hip). With with_stats false
-// the statistics pass is skipped: the caller has written its partials (column sums of K and column max |V| of each
-// 32-token half of each 64-token block, [layers][batch * heads][blocks][2][128] each) at the start of the workspace.
+// the statistics pass is skipped: the caller has written the column sums of K of each 32-token half of each 64-token
+// block ([layers][batch * heads][blocks][2][128] fp32) at the start of the workspace, and V is quantised in the last
+// pass with K.
 int kv_requant_check(int64_t layers, int64_t batch, int64_t len, int64_t heads, const int8_t* k8,
                      const float* k_scale, const float* km, const uint8_t* v8, const uint8_t* v8lo,
-                     const float* v_scale, int64_t slots, int64_t cap, int64_t slot);
+                     const uint8_t* v_scale, int64_t slots, int64_t cap, int64_t slot);
 int kv_requant_launch(bool with_stats, bool f16, const uint16_t* k, const uint16_t* v, int64_t layers, int64_t batch,
                       int64_t len, int64_t heads, int64_t k_s_layer, int64_t k_s_batch, int64_t k_s_tok,
                       int64_t k_s_head, int64_t v_s_layer, int64_t v_s_batch, int64_t v_s_tok, int64_t v_s_head,
-                      int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale,
+                      int8_t* k8, float* k_scale, float* km, uint8_t* v8, uint8_t* v8lo, uint8_t* v_scale,
                       int64_t slots, int64_t cap, int64_t slot, void* workspace, void* stream);
 
 // Position of key k (0..63) inside a 64-key fp8 V block.

@@ -4,9 +4,9 @@
 //   norm_rope_q_kernel:  q projection -> RMSNorm (times its weight) -> rope -> int8 Q per 32-row group with its
 //                        scale, the per-chunk logit bias q . km_c, and (optionally) the roped bf16 Q.
 //   norm_rope_k_kernel:  k projection -> RMSNorm -> rope -> the roped bf16 K, plus, per 32-token half of each
-//                        64-token block, the fp32 column sums of the roped K and the column max |V|: the partials
-//                        the re-quant's own statistics pass would write, in its order, so its finaliser and
-//                        quantiser finish the job.
+//                        64-token block, the fp32 column sums of the roped K: the partials the re-quant's own
+//                        statistics pass would write, in its order, so its finaliser and quantiser finish the job
+//                        (the quantiser reads V and quantises it with K).
 //
 // A workgroup has one wave per head and takes 32 token rows. Lane (rq, g) = (lane >> 4, lane & 15)
 // of wave h holds channels 8 g .. 8 g + 7 of head h in rows 4 (rq + 4 s) + j, s = 0, 1, j = 0..3 (four
@@ -34,7 +34,6 @@ struct ProArgs {
   int64_t len, heads, bh;
   int64_t x_sb, x_st;          // projection strides (elements): batch, token; its heads * 128 channels contiguous
   int64_t o_sb, o_st, o_sh;    // roped output strides
-  int64_t v_sb, v_st, v_sh;    // V strides (K kernel)
   int64_t frame_tokens, gw, start_frame;
   int64_t lp, nb;              // Q rows padded to the attention tile (Q); 64-token blocks of the chunk (K)
   float eps;
@@ -231,15 +230,13 @@ __global__ __launch_bounds__(MAXT) void norm_rope_q_kernel(const uint16_t* __res
   }
 }
 
-// Workgroup (32-token half of a 64-token block, batch): one wave per head. Writes that half's partials.
+// Workgroup (32-token half of a 64-token block, batch): one wave per head. Writes that half's column sums of K.
 template <int MAXT>
 __global__ __launch_bounds__(MAXT) void norm_rope_k_kernel(const uint16_t* __restrict__ k,
-                                                           const uint16_t* __restrict__ v,
                                                            const uint16_t* __restrict__ w,
                                                            const double2* __restrict__ tab, ProArgs a,
                                                            uint16_t* __restrict__ k_out,
-                                                           float* __restrict__ part_sum,
-                                                           float* __restrict__ part_amax) {
+                                                           float* __restrict__ part_sum) {
   __shared__ double2 s_cs[PR * RP];
   __shared__ double s_ss[PR * PRO_MAX_HEADS];
   __shared__ float s_r[PR];
@@ -249,39 +246,9 @@ __global__ __launch_bounds__(MAXT) void norm_rope_k_kernel(const uint16_t* __res
   const int64_t row0 = (int64_t)half * PR;
   uint32_t x[2][4][4];
   load_rows(x, k + b * a.x_sb, a, row0);
-  // the V rows go out with the K rows; V is neither normed nor roped, so its column max |V| is taken (and
-  // written) as soon as they land, before the rope needs the registers
-  v4i vw[2][4];
-  const uint16_t* vp = v + b * a.v_sb + h * a.v_sh + g * 8;
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t t = row0 + 4 * (rq + 4 * s) + j;
-      vw[s][j] = t < a.len ? *(const v4i*)(vp + (uint32_t)t * (uint32_t)a.v_st) : v4i{0, 0, 0, 0};
-    }
   stage_rope(s_cs, tab, a, row0);
   // partials [batch * heads][blocks][2 halves][128]: half index = blockIdx.x
   const int64_t o = (((int64_t)b * a.heads + h) * a.nb * 2 + half) * D + g * 8;
-  {   // column max |V| of the half: lane (rq, g) over its 8 rows, then over rq (lanes g + 16 rq)
-    float vmax[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vmax[e] = 0.f;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          vmax[2 * q] = fmaxf(vmax[2 * q], fabsf(bf_lo((uint32_t)vw[s][j][q])));
-          vmax[2 * q + 1] = fmaxf(vmax[2 * q + 1], fabsf(bf_hi((uint32_t)vw[s][j][q])));
-        }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) vmax[e] = max_xor32(max_xor16(vmax[e]));
-    if (rq == 0)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) part_amax[o + e] = vmax[e];
-  }
   norm_rope_rows(x, w, a, row0, s_ss, s_r, s_cs);
   uint16_t* ko = k_out + b * a.o_sb + h * a.o_sh + g * 8;
 #pragma unroll
@@ -339,7 +306,6 @@ static int prologue_args(ProArgs& a, int64_t batch, int64_t len, int64_t heads, 
   a.len = len; a.heads = heads; a.bh = batch * heads;
   a.x_sb = s_batch; a.x_st = s_tok;
   a.o_sb = a.o_st = a.o_sh = 0;
-  a.v_sb = a.v_st = a.v_sh = 0;
   a.frame_tokens = frame_tokens; a.gw = grid_w; a.start_frame = start_frame;
   a.lp = 0; a.nb = 0;
   a.eps = eps;
@@ -400,7 +366,7 @@ extern "C" int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, in
                                         const double* rope, int64_t rope_rows, int64_t grid_h, int64_t grid_w,
                                         int64_t start_frame, uint16_t* k_out, int64_t o_s_batch,
                                         int64_t o_s_tok, int64_t o_s_head, int8_t* k8, float* k_scale,
-                                        float* km, uint8_t* v8, uint8_t* v8lo, float* v_scale, int64_t slots,
+                                        float* km, uint8_t* v8, uint8_t* v8lo, uint8_t* v_scale, int64_t slots,
                                         int64_t cap, int64_t slot, void* workspace, void* stream) {
   ProArgs a;
   if (const int st = prologue_args(a, batch, len, heads, k, k_s_batch, k_s_tok, norm_weight, eps, rope, rope_rows,
@@ -414,7 +380,6 @@ extern "C" int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, in
       (len + KB) * o_s_tok >= ((int64_t)1 << 31))
     return LBW_E_SHAPE;
   a.o_sb = o_s_batch; a.o_st = o_s_tok; a.o_sh = o_s_head;
-  a.v_sb = v_s_batch; a.v_st = v_s_tok; a.v_sh = v_s_head;
   a.nb = (len + KB - 1) / KB;
   if (a.nb > 0x7fffffff) return LBW_E_SHAPE;
   // the re-quant's own checks (shape, slot, ring pointers) run before anything is launched
@@ -422,14 +387,13 @@ extern "C" int lbw_norm_rope_kv_requant(const uint16_t* k, const uint16_t* v, in
     return st;
   if (const int dv = check_device()) return dv;
   float* part_sum = (float*)workspace;
-  float* part_amax = part_sum + a.bh * a.nb * 2 * D;
   const dim3 grid((unsigned)(2 * a.nb), (unsigned)batch), block(64 * (unsigned)heads);
   if (heads <= 12)
-    hipLaunchKernelGGL(norm_rope_k_kernel<768>, grid, block, 0, (hipStream_t)stream, k, v, norm_weight,
-                       (const double2*)rope, a, k_out, part_sum, part_amax);
+    hipLaunchKernelGGL(norm_rope_k_kernel<768>, grid, block, 0, (hipStream_t)stream, k, norm_weight,
+                       (const double2*)rope, a, k_out, part_sum);
   else
-    hipLaunchKernelGGL(norm_rope_k_kernel<1024>, grid, block, 0, (hipStream_t)stream, k, v, norm_weight,
-                       (const double2*)rope, a, k_out, part_sum, part_amax);
+    hipLaunchKernelGGL(norm_rope_k_kernel<1024>, grid, block, 0, (hipStream_t)stream, k, norm_weight,
+                       (const double2*)rope, a, k_out, part_sum);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return kv_requant_launch(false, false, k_out, v, 1, batch, len, heads, 0, o_s_batch, o_s_tok, o_s_head, 0, v_s_batch,
                            v_s_tok, v_s_head, k8, k_scale, km, v8, v8lo, v_scale, slots, cap, slot, workspace,

@@ -11,6 +11,7 @@ K_BLOCK = 64
 Q_TILE = 256
 Q_GROUP = 32
 MAX_SEGMENTS = 8
+V_TABLE_BYTES = 256   # E8M0 V scales per 64-key block: 2 key groups x 128 channels
 ctypes_i32 = ctypes.c_int32
 
 
@@ -60,7 +61,8 @@ class RingCache:
 
     Device layout (include/lbw_attn.h): k8 int8 [L, S, BH, cap, 128]; k_scale fp32 [L, S, BH, cap/64];
     km fp32 [L, S, BH, 128]; v8 (and, with v_terms=2, the residual plane v8lo) uint8 [L, S, BH, cap/64, 128, 64];
-    v_scale fp32 [L, S, BH, 128].
+    v_scale uint8 [L, S, BH, cap/64, 256], the E8M0 V scales of each 64-key block (byte (32 g + c % 32) * 4 + c / 32
+    = 127 + e for channel c and key group g, the keys 32 g .. 32 g + 31 of the block).
     """
 
     def __init__(self, layers, batch, heads, cap, slots, device, v_terms=2, zero=True):
@@ -81,8 +83,9 @@ class RingCache:
         self.v8 = new(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev)
         self.v8lo = new(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev) \
             if v_terms == 2 else None
-        self.v_scale = (torch.ones if zero else torch.empty)(layers, slots, bh, HEAD_DIM, dtype=torch.float32,
-                                                             device=dev)
+        self.v_scale = torch.empty(layers, slots, bh, nb, V_TABLE_BYTES, dtype=torch.uint8, device=dev)
+        if zero:
+            self.v_scale.fill_(127)   # scale 1
         self.device = dev
 
     @property

@@ -5,14 +5,15 @@ The reference keeps quantised K/V in a layer's cache dict next to the bf16 windo
 ([B, kv_size, H, D], the buffers of lingbot/layers/kv_cache.py), re-quantises the attended slice on a chunk's
 first forward (`requant_all`), quantises only the newly written tokens on the others (`write_chunk`), and attends
 with only Q quantised per call (`attend`). Here the quantised slice is one slot of a one-layer ring cache
-(int8 K - mean per 64-token block, e4m3 V per channel plus the residual plane; the layout of include/lbw_attn.h),
+(int8 K - mean per 64-token block, e4m3 V with a power-of-two scale per channel and 32-token half-block, plus the
+residual plane; the layout of include/lbw_attn.h),
 kept under the dict keys "lbw_ring" and "lbw_ws".
 
 One difference, by design: the reference's write_chunk quantises [floor64(start), end) against the mean and V
 scale frozen by the last requant_all, with a 1.5x V margin and a clamp for tokens past it (sage_kvq.py:29-35,
 78-90), because its re-quant ran in torch. Here write_chunk re-quantises the whole slice [0, end) with fresh
-statistics (the 30-layer re-quant of a 6032-token chunk takes ~0.6 ms on MI355X, one layer ~0.02 ms), so every
-token is quantised against its own slice's mean and V scale and nothing saturates.
+statistics (the 30-layer re-quant of a 6032-token chunk takes ~0.5 ms on MI355X, one layer ~0.02 ms), so every
+token is quantised against its own slice's mean and V scales and nothing saturates.
 """
 import torch
 
@@ -44,8 +45,8 @@ def release(kv_cache):
 
 def requant_all(cache, kv_len, margin=None):
     """Fresh K mean and V scales over the attended slice cache["k"/"v"][:, :kv_len], then quantise all of it
-    (sage_kvq.py:93-98). `margin` is accepted for the reference's signature; the per-channel V scale here is the
-    power of two above the slice's own amax, so no margin is needed."""
+    (sage_kvq.py:93-98). `margin` is accepted for the reference's signature; each V scale here is the power of two
+    above its own half-block's amax, so no margin is needed."""
     del margin
     k, v = cache["k"][:, :kv_len], cache["v"][:, :kv_len]
     kernels.kv_requant(k, v, cache["lbw_ring"], 0, workspace=cache["lbw_ws"])

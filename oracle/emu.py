@@ -12,18 +12,20 @@ quantisers and its documentation of the fused kernel:
   `k.mean(dim=1)` on such a tensor is (lingbot/layers/sage_preq.py:115; sage_kvq.py:85, :96), then int8 per
   64-token block as above;
   tokens past the chunk count as zero after the subtraction (sage_kvq.py:61-63).
-- V: fp8 e4m3 with one scale per (head, channel) (sage_kvq.py:69-75; sage_preq.py:47-78). The reference maps
-  amax to 2.25 because its PV accumulates in fp16 (sage_kvq.py:30-31); the MFMA here accumulates in fp32, so
-  the scale is the power of two 2^e that takes amax into (224, 448], the top binade of e4m3: V / 2^e is exact,
-  e4m3's relative precision is the same in every binade, and a power-of-two scale can ride on the fp8 MFMA's
-  E8M0 block-scale operand instead of a multiply of the accumulator.
+- V: fp8 e4m3 with per-channel scales (sage_kvq.py:69-75; sage_preq.py:47-78), here one per (head, channel) for
+  each 32-key half of a 64-key block. The reference maps the channel's amax to 2.25 because its PV accumulates
+  in fp16 (sage_kvq.py:30-31); the MFMA here accumulates in fp32, so the scale is the power of two 2^e that takes
+  the group's amax into (224, 448], the top binade of e4m3: V / 2^e is exact, e4m3's relative precision is the
+  same in every binade, and a power-of-two scale rides on the fp8 MFMA's E8M0 block-scale operand (per A row and
+  32-key block) instead of a multiply of the accumulator. A group's scale needs only its own block, so a chunk's
+  V is quantised in one pass over it.
 - Logits: S = q8 . k8 in int32 (experiments/bench_attn/h2_tiles/README.md:45), dequantised with
   q_scale * k_scale * sm_scale * log2(e) into the exp2 domain; P = exp2(s - m + 8.807) <= 448 cast to e4m3
   (experiments/bench_attn/phi_calib.md:11-16); O = sum P V / sum P, with the V scale
   (h2_tiles/README.md:13-20; experiments/bench_attn/splitkv/README.md:62-63). The reference max m of a row
   moves only when a block's max passes it by more than RESCALE_SLACK, so the rescale of the accumulated O is
-  rare; each block's contribution is accumulated in true V units (its chunk's power-of-two V scale applied), so
-  a switch between chunks with different V scales needs no rescale.
+  rare; each block's contribution is accumulated in true V units (its power-of-two group scales applied by the
+  MFMA), so nothing is rescaled between blocks or chunks.
 - Memory chunks keep their own mean and V scale; the bias q . mean_c of chunk c is added to its logits
   (a constant per (query, chunk), so it drops out when there is only one chunk).
 
@@ -164,38 +166,66 @@ def quant_k(k, km):
     return k8.view(h, lp, d), ks
 
 
-def v_scale_of(v):
-    """v bf16 [L, H, D] -> (v_scale, recip) fp32 [H, D]: the power of two 2^e with amax / 2^e in (224, 448]
-    (amax floored at 1e-7), and 2^-e. With amax = f * 2^x, f in [0.5, 1): e = x - 9 when f <= 0.875 (448 =
-    0.875 * 2^9), else x - 8 -- integer arithmetic on the exponent, no rounding."""
-    v = _as_lhd(v)
-    amax = v.float().abs().amax(dim=0).clamp_min(AMAX_FLOOR)
-    f, x = torch.frexp(amax)
-    e = torch.where(f <= 0.875, x - 9, x - 8)
-    one = torch.ones_like(amax)
-    return torch.ldexp(one, e), torch.ldexp(one, -e)
+V_GROUP_OF_KEY = np.arange(K_BLOCK) >> 5   # key group of in-block key k: its 32-key half (see quant_v)
 
 
-def quant_v(v):
-    """v bf16 [L, H, D] -> (v8, v8lo uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, v_scale fp32 [H, D]).
-
-    Two e4m3 terms: y = v / v_scale (exact: a power of two, |y| <= 448); hi = e4m3(y); lo = e4m3((y - hi) * 16),
-    so v ~ (hi + lo / 16) * v_scale. y - hi is exact in fp32 (hi is y rounded to 3 mantissa bits) and
-    |y - hi| * 16 <= 256 stays in range."""
+def v_group_exponents(v):
+    """v [L, H, D] -> e int64 [H, nb, 2, D]: per 64-key block, key group g and channel, the exponent of the power of
+    two 2^e with amax / 2^e in (224, 448], amax over the group's 32 keys (padding tokens count as zero; floored at
+    1e-7). With amax = f * 2^x, f in [0.5, 1): e = x - 9 when f <= 0.875 (448 = 0.875 * 2^9), else x - 8 -- integer
+    arithmetic on the exponent, no rounding."""
     v = _as_lhd(v)
     n, h, d = v.shape
     lp = pad_to(n, K_BLOCK)
-    vs, recip = v_scale_of(v)
+    x = torch.zeros(h, lp, d, dtype=torch.float32)
+    x[:, :n] = v.float().abs().permute(1, 0, 2)
+    x = x.view(h, lp // K_BLOCK, K_BLOCK, d)
+    grp = torch.from_numpy(V_GROUP_OF_KEY)
+    amax = torch.stack([x[:, :, grp == g].amax(dim=2) for g in (0, 1)], dim=2).clamp_min(AMAX_FLOOR)
+    f, ex = torch.frexp(amax)
+    return torch.where(f <= 0.875, ex - 9, ex - 8).long()
+
+
+def v_scale_table(e):
+    """e [H, nb, 2, D] -> the E8M0 scale bytes uint8 [H, nb, 256] of each block in the attention's lane order:
+    byte (32 g + lq) * 4 + mt = 127 + e[g][32 mt + lq], the scale of channel 32 mt + lq for the keys of group g."""
+    h, nb = e.shape[:2]
+    t = (e + 127).view(h, nb, 2, 4, 32)               # [h, b, g, mt, lq]: channel = 32 mt + lq
+    return t.permute(0, 1, 2, 4, 3).reshape(h, nb, 256).to(torch.uint8)
+
+
+def v_exponents_of_table(table):
+    """Inverse of v_scale_table: uint8 [H, nb, 256] -> e int64 [H, nb, 2, D]."""
+    h, nb = table.shape[:2]
+    return table.long().view(h, nb, 2, 32, 4).permute(0, 1, 2, 4, 3).reshape(h, nb, 2, HEAD_DIM) - 127
+
+
+def quant_v(v):
+    """v bf16 / fp16 [L, H, D] -> (v8, v8lo uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, the E8M0
+    scale table uint8 [H, nb, 256] of v_scale_table).
+
+    Scales are powers of two, one per (64-key block, key group, channel): group g of a block holds its keys
+    32 g .. 32 g + 31, the 32-deep K-block g of the 64-deep fp8 PV MFMA (bytes 16 g .. 16 g + 15 of every lane's
+    operand, which the permuted layout fills with those keys), whose E8M0 block scale of the A operand applies per
+    row and K-block -- so the MFMA applies the scale itself. Two e4m3
+    terms: y = v / 2^e (exact, |y| <= 448); hi = e4m3(y); lo = e4m3((y - hi) * 16), so v ~ (hi + lo / 16) * 2^e.
+    y - hi is exact in fp32 (hi is y rounded to 3 mantissa bits) and |y - hi| * 16 <= 256 stays in range."""
+    v = _as_lhd(v)
+    n, h, d = v.shape
+    lp = pad_to(n, K_BLOCK)
+    e = v_group_exponents(v)
+    per_key = e[:, :, torch.from_numpy(V_GROUP_OF_KEY)]                  # [h, nb, 64 keys, d]
+    recip = torch.ldexp(torch.ones(per_key.shape), -per_key).view(h, lp, d)
     y = torch.zeros(h, lp, d, dtype=torch.float32)
-    y[:, :n] = v.float().permute(1, 0, 2) * recip[:, None, :]
-    y = y.clamp(-V_MAX, V_MAX)
+    y[:, :n] = v.float().permute(1, 0, 2)
+    y = (y * recip).clamp(-V_MAX, V_MAX)
     hi = e4m3_encode(y)
     lo = e4m3_encode((y - e4m3_decode(hi)) * V_LO_SCALE)
     planes = []
     for bits in (hi, lo):
         bits = bits.view(h, lp // K_BLOCK, K_BLOCK, d)[:, :, torch.from_numpy(V_KEY_OF_POS)]   # [h, b, pos, d]
         planes.append(bits.permute(0, 1, 3, 2).contiguous())
-    return planes[0], planes[1], vs
+    return planes[0], planes[1], v_scale_table(e)
 
 
 def requant(k, v):
@@ -217,17 +247,20 @@ def span(chunk):
 
 
 def dequant_v(chunk, terms=None):
-    """e4m3 V of a quantised chunk back to fp32 [H, first + n, D] in key order (slot keys 0 .. first + n - 1),
-    without the V scale: hi + lo / 16 (or hi alone with terms=1, the default for a chunk whose "v8lo" is None)."""
+    """e4m3 V of a quantised chunk back to fp32 [H, first + n, D] in key order (slot keys 0 .. first + n - 1), in
+    true units: (hi + lo / 16) * 2^e with each key's group scale (or hi alone with terms=1, the default for a
+    chunk whose "v8lo" is None)."""
     if terms is None:   # a chunk quantised without the residual plane has one term
         terms = V_TERMS if chunk.get("v8lo") is not None else 1
     h, nb, d, _ = chunk["v8"].shape
     end = chunk.get("first", 0) + chunk["n"]
+    e = v_exponents_of_table(chunk["v_scale"])[:, :, torch.from_numpy(V_GROUP_OF_KEY)]   # [h, nb, key, d]
+    scale = torch.ldexp(torch.ones(e.shape), e)
     out = 0
     for bits, w in ((chunk["v8"], 1.0), (chunk["v8lo"], 1.0 / V_LO_SCALE))[:terms]:
         vals = e4m3_decode(bits)[:, :, :, torch.from_numpy(V_POS_OF_KEY)]   # [h, nb, d, key]
-        out = out + vals.permute(0, 1, 3, 2).reshape(h, nb * K_BLOCK, d)[:, :end] * w
-    return out
+        out = out + vals.permute(0, 1, 3, 2) * w
+    return (out * scale).reshape(h, nb * K_BLOCK, d)[:, :end]
 
 
 def qk_logits(q8, k8):
@@ -289,7 +322,6 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
         if j + nbc <= j0 or j >= j1:
             j += nbc
             continue
-        vs = c["v_scale"][hh]
         beta = beta_of(ci)
         for b in range(max(0, j0 - j), min(nbc, j1 - j)):
             sb = b0 + b   # the slot's block
@@ -309,8 +341,8 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
             p = torch.exp2(x)
             l_run = l_run + p.sum(dim=1)
             pr = e4m3_decode(e4m3_encode(p)) if p_round else p
-            # the chunk's V scale is a power of two: exact, and the same factor the MFMA's block scale applies
-            o = o + torch.matmul(pr, vdec[ci][hh, k0:k1]) * vs[None, :]
+            # V in true units: its group scales are powers of two, exact, the factors the MFMA's block scale applies
+            o = o + torch.matmul(pr, vdec[ci][hh, k0:k1])
         j += nbc
     return o, m_run, l_run
 
@@ -321,7 +353,7 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
     slot's 64-key blocks in sequence (keys outside the read range masked), a reference row max m, and per block
       b = max_j S_ij * cb + beta,  m_new = b if b > m + tau else m,  alpha = exp2(m - m_new),
       o = alpha * o,  l = alpha * l,  P_ij = exp2(S_ij * cb + beta - m_new + 8.807 - tau)  (<= 448),
-      l += sum P,  o += (e4m3(P) . V8) * v_scale,
+      l += sum P,  o += e4m3(P) . (V8 * 2^e)  (V in true units, its group scales applied),
     with cb = q_scale * k_scale * sm_scale * log2(e) and beta = q . mean_k of the chunk (several chunks only);
     finally out = o / l. Each block's contribution is in true V units, so a chunk switch needs no rescale.
     With `schedule_gx` (the kernel's workgroups per XCD), tiles the kernel splits between workgroups are
@@ -407,7 +439,7 @@ def attention_exact_max(q, chunks, sm_scale=None, q_block=1024):
                 p = torch.exp2(logits[ci] - m[:, None] + P_OFFSET)
                 den = den + p.sum(dim=1)
                 p8 = e4m3_decode(e4m3_encode(p))
-                num = num + torch.matmul(p8, vdec[ci][hh, c.get("first", 0):]) * c["v_scale"][hh][None, :]
+                num = num + torch.matmul(p8, vdec[ci][hh, c.get("first", 0):])
             out[a:e, hh] = num / den[:, None]
     return out
 

@@ -62,8 +62,8 @@ def test_requant_workspace_formula(lib):
     for layers, bh, n in ((1, 1, 1), (30, 24, 1508), (2, 3, 64), (1, 5, 65), (30, 12, 6032), (1, 1, 262400)):
         nb = -(-n // 64)
         g = layers * bh
-        # column sums and maxima per 32-token half-block, plus the per-channel V reciprocals
-        assert lib.lbw_kv_requant_workspace_bytes(layers, bh, n) == (2 * g * 2 * nb * 128 + g * 128) * 4
+        # the K column sums of each 32-token half-block (V is quantised without a workspace)
+        assert lib.lbw_kv_requant_workspace_bytes(layers, bh, n) == g * 2 * nb * 128 * 4
     assert lib.lbw_kv_requant_workspace_bytes(0, 1, 1) == 0
 
 

@@ -16,7 +16,7 @@ def test_ring_layout_sizes():
     assert r.k_scale.shape == (3, 4, 10, 3)
     assert r.km.shape == (3, 4, 10, 128)
     assert r.v8.shape == r.v8lo.shape == (3, 4, 10, 3, 128, 64)
-    assert r.v_scale.shape == (3, 4, 10, 128)
+    assert r.v_scale.shape == (3, 4, 10, 3, 256) and r.v_scale.dtype == torch.uint8
     assert kernels.RingCache(1, 1, 1, 64, 2, "cpu", v_terms=1).v8lo is None
     with pytest.raises(ValueError):
         kernels.RingCache(1, 1, 1, 100, 2, "cpu")

@@ -162,18 +162,43 @@ def test_smoothing_makes_k8_invariant_to_channel_offsets():
 
 def test_v_scale_power_of_two_edges():
     """The exponent rule at the binade edges: amax exactly 448 * 2^e keeps e; one bf16 step above moves to e + 1;
-    an all-zero channel uses the 1e-7 floor."""
+    an all-zero group uses the 1e-7 floor."""
     vals = torch.tensor([448.0, 450.0, 224.0, 225.0, 1.0, 3.5, 0.0])   # 450: the bf16 value after 448
-    v = torch.zeros(4, 1, len(vals))
-    v[1, 0] = vals
-    vs, recip = emu.v_scale_of(v.to(torch.bfloat16))
+    v = torch.zeros(64, 1, len(vals))
+    v[1, 0] = vals                                                     # key 1 is in group 0; group 1 stays zero
+    e = emu.v_group_exponents(v.to(torch.bfloat16))
+    assert e.shape == (1, 1, 2, len(vals))
     want = [1.0, 2.0, 0.5, 1.0, 2.0 ** -8, 2.0 ** -7, None]   # 3.5 = 448 * 2^-7 exactly
-    for got, w, a in zip(vs[0].tolist(), want, vals.tolist()):
+    for got, w, a in zip(torch.ldexp(torch.ones(len(vals)), e[0, 0, 0]).tolist(), want, vals.tolist()):
         if w is not None:
             assert got == w, (a, got, w)
-    floor_scale = vs[0, -1].item()
-    assert 224 < 1e-7 / floor_scale <= 448
-    assert torch.all(vs * recip == 1)
+    for floor_scale in (2.0 ** e[0, 0, 0, -1].item(), 2.0 ** e[0, 0, 1, 0].item()):
+        assert 224 < 1e-7 / floor_scale <= 448
+
+
+def test_v_groups_and_scale_table_layout():
+    """Group g is the keys 32 g .. 32 g + 31 of a block: a large value at key 32 (group 1) moves group 1's exponent
+    only. The table holds 127 + e[g][c] at byte (32 g + c % 32) * 4 + c // 32 (checked entry by entry), and
+    v_exponents_of_table inverts it. The groups are the positions 16 g .. 16 g + 15 and 32 + 16 g .. 32 + 16 g + 15
+    of the permuted layout: bytes 16 g .. 16 g + 15 of each lane's PV operand, the MFMA's K-block g."""
+    assert emu.V_GROUP_OF_KEY.tolist() == [0] * 32 + [1] * 32
+    for g in range(2):
+        pos = [int(emu.V_POS_OF_KEY[k]) for k in range(64) if emu.V_GROUP_OF_KEY[k] == g]
+        assert sorted(pos) == list(range(16 * g, 16 * g + 16)) + list(range(32 + 16 * g, 48 + 16 * g))
+    v = torch.ones(64, 1, 128)
+    v[32, 0, 7] = 100.0
+    e = emu.v_group_exponents(v.to(torch.bfloat16))
+    assert e[0, 0, 1, 7] > e[0, 0, 0, 7] and torch.all(e[0, 0, 0] == e[0, 0, 0, 0])
+    assert torch.all(e[0, 0, 1, :7] == e[0, 0, 0, 0]) and torch.all(e[0, 0, 1, 8:] == e[0, 0, 0, 0])
+    rng = np.random.default_rng(9)
+    e = torch.from_numpy(rng.integers(-40, 40, size=(2, 3, 2, 128)))
+    t = emu.v_scale_table(e)
+    for hh in range(2):
+        for b in range(3):
+            for g in range(2):
+                for c in range(128):
+                    assert int(t[hh, b, (32 * g + c % 32) * 4 + c // 32]) == 127 + int(e[hh, b, g, c])
+    assert torch.equal(emu.v_exponents_of_table(t), e)
 
 
 def test_v_position_map_is_a_bijection():
@@ -185,17 +210,25 @@ def test_v_quant_layout_and_two_term_bound():
     torch.manual_seed(4)
     n, h = 130, 2
     v = (torch.randn(n, h, 128) * torch.rand(1, h, 128) * 4).to(torch.bfloat16)
-    v8, v8lo, vs = emu.quant_v(v)
-    assert v8.shape == (h, 3, 128, 64)
-    amax = v.float().abs().amax(dim=0)
-    # the scale is a power of two taking the channel max into e4m3's top binade (224, 448]
-    mant, _ = torch.frexp(vs)
-    assert torch.all(mant == 0.5)
-    assert torch.all(amax / vs <= 448) and torch.all(amax / vs > 224)
-    y = v.float().permute(1, 0, 2) / vs[:, None, :]   # [h, n, d], exact
-    chunk = {"v8": v8, "v8lo": v8lo, "n": n}
-    one = emu.dequant_v(chunk, terms=1)
-    two = emu.dequant_v(chunk, terms=2)
+    v8, v8lo, table = emu.quant_v(v)
+    assert v8.shape == (h, 3, 128, 64) and table.shape == (h, 3, 256)
+    # each key's scale, from the group amax computed here directly (keys 32 g .. 32 g + 31 of block b)
+    vp = torch.zeros(192, h, 128)
+    vp[:n] = v.float()
+    scale = torch.empty(h, 192, 128)
+    for b in range(3):
+        for g in range(2):
+            keys = [64 * b + k for k in range(32 * g, 32 * g + 32)]
+            amax = vp[keys].abs().amax(dim=0).clamp_min(1e-7)                # [h, d]
+            s = 2.0 ** torch.ceil(torch.log2(amax.double() / 448)).float()   # the power of two: amax / s in (224, 448]
+            assert torch.all(amax / s <= 448) and torch.all(amax / s > 224)
+            scale[:, keys] = s[:, None, :]
+            e = emu.v_exponents_of_table(table)[:, b, g]
+            assert torch.equal(torch.ldexp(torch.ones(h, 128), e), s)
+    y = v.float().permute(1, 0, 2) / scale[:, :n]   # [h, n, d], exact
+    chunk = {"v8": v8, "v8lo": v8lo, "v_scale": table, "n": n}
+    one = emu.dequant_v(chunk, terms=1) / scale[:, :n]
+    two = emu.dequant_v(chunk, terms=2) / scale[:, :n]
     # one e4m3 term: half an e4m3 step (2^-4 relative, 2^-10 absolute in the subnormal range)
     tol1 = torch.maximum(y.abs() * 2.0 ** -4, torch.full_like(y, 2.0 ** -10))
     assert torch.all((one - y).abs() <= tol1)
@@ -203,10 +236,6 @@ def test_v_quant_layout_and_two_term_bound():
     tol2 = torch.maximum(y.abs() * 2.0 ** -8, torch.full_like(y, 2.0 ** -13))
     assert torch.all((two - y).abs() <= tol2)
     assert (two - y).abs().mean() < (one - y).abs().mean() / 8
-    # the channel max lands in the top binade
-    pos = y.abs().argmax(dim=1)
-    top = one.gather(1, pos[:, None, :]).abs()
-    assert torch.all(top >= 224) and torch.all(top <= 448)
 
 
 # ---------------------------------------------------------------- logits
@@ -302,7 +331,7 @@ def test_schedule_covers_every_block_once():
 
 def _ragged_chunks(seed, lens=(200, 150, 333), h=2, lq=300):
     """Chunks with their own K offsets (so the per-chunk means and the logit bias differ) and V amplitudes (so
-    the V scales differ, exercising the accumulator's rescale at each chunk switch)."""
+    the V group scales differ from chunk to chunk)."""
     g = torch.Generator().manual_seed(seed)
     ks, vs = [], []
     for i, n in enumerate(lens):
@@ -315,7 +344,8 @@ def _ragged_chunks(seed, lens=(200, 150, 333), h=2, lq=300):
 
 def _direct_softmax_fp64(q, chunks, sm_scale=None):
     """Exact softmax attention of the dequantised logits and V in fp64, one row at a time in closed form:
-    logit = q8.k8 * q_scale * k_scale + q.km_c (several chunks), base-e softmax, O = sum P V v_scale / sum P.
+    logit = q8.k8 * q_scale * k_scale + q.km_c (several chunks), base-e softmax, O = sum P V / sum P with V
+    dequantised to true units (its group scales applied).
     No block order, no running max, no split: what the online form must equal when P is not rounded."""
     q = q[0]
     lq, h, d = q.shape
@@ -332,7 +362,7 @@ def _direct_softmax_fp64(q, chunks, sm_scale=None):
             if len(chunks) > 1:
                 s = s + (q[:, hh].double() @ c["km"][hh].double())[:, None]
             logits.append(s * sm)
-            vals.append(emu.dequant_v(c)[hh, a:a + n].double() * c["v_scale"][hh].double()[None, :])
+            vals.append(emu.dequant_v(c)[hh, a:a + n].double())
         s = torch.cat(logits, dim=1)
         p = torch.softmax(s, dim=1)
         out[:, hh] = p @ torch.cat(vals, dim=0)
