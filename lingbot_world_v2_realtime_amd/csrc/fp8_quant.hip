@@ -3,8 +3,11 @@
 // output row) and its activations (every call, per token). The GEMM itself is a plain rowwise-scaled FP8 GEMM
 // (hipBLASLt); this kernel is the part around it that runs on every call.
 //
-// One workgroup per row: 256 threads, 16-byte loads. Rows of up to 16384 values stay in registers between the
-// amax and the quantisation (one read); longer rows are read twice (the second read from the cache).
+// Many rows of up to 4096 values: one wave per row (a one-wave workgroup), the row's amax within the wave (no
+// barrier): 5.7 against 6.4 us for 6032 x 1536 bf16 on MI355X. Otherwise one workgroup per row, 256 threads, more
+// loads in flight per row (2.05 against 2.4 us for 333 x 1536); rows of up to 16384 values stay in registers
+// between the amax and the quantisation (one read), longer ones are read twice (the second read from the cache).
+// 16-byte loads.
 #include "lbw_common.h"
 
 #pragma clang fp contract(off)
@@ -92,6 +95,40 @@ __device__ __forceinline__ float row_scale(uint32_t amax_bits, uint32_t* s_red, 
   return sc;
 }
 
+// Rows of at most NCH * 512 values, a one-wave workgroup each: lane l holds 8-value chunks l, l + 64, ... in
+// registers. The same amax, scale and quotients as the workgroup-per-row kernels.
+template <typename T, int NCH>
+__global__ __launch_bounds__(64) void quant_rows_fp8_wave_kernel(const T* __restrict__ x, int64_t cols, int64_t s_row,
+                                                                 uint8_t* __restrict__ x8, float* __restrict__ scale) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const T* xr = x + row * s_row;
+  float f[NCH][8];
+  uint32_t amax = 0;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = 8 * (int64_t)(lane + 64 * i);
+    if (c < cols) {
+      Row8<T>::load(xr + c, f[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = max(amax, abs_bits(f[i][e]));
+  }
+  const float q = __fdiv_rn(__uint_as_float(wave_max_u32(amax)), FP8_MAX);
+  const float sc = q < FP8_SCALE_FLOOR ? FP8_SCALE_FLOOR : q;
+  if (lane == 0) scale[row] = sc;
+  const float r = __fdiv_rn(1.f, sc);
+  uint8_t* outr = x8 + row * cols;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int64_t c = 8 * (int64_t)(lane + 64 * i);
+    if (c < cols) *(uint2*)(outr + c) = quant8(f[i], sc, r);
+  }
+}
+
 // Rows of at most NCH * 2048 values: thread t holds 8-value chunks t, t + 256, ... in registers.
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict__ x, int64_t cols, int64_t s_row,
@@ -154,6 +191,21 @@ template <typename T>
 static void launch_quant_rows(const T* x, int64_t rows, int64_t cols, int64_t s_row, uint8_t* x8, float* scale,
                               hipStream_t stream) {
   const dim3 grid((unsigned)rows), block(256);
+  if (cols <= 4096 && rows >= 2048) {
+    const dim3 wblock(64);
+    const int64_t wch = (cols + 511) / 512;
+    if (wch <= 1)
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 1>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+    else if (wch <= 2)
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 2>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+    else if (wch <= 3)
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 3>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+    else if (wch <= 4)
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 4>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+    else
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 8>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+    return;
+  }
   const int64_t nch = (cols + 2047) / 2048;
   if (nch <= 1)
     hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 1>), grid, block, 0, stream, x, cols, s_row, x8, scale);

@@ -20,7 +20,9 @@ def _k():
 @pytest.mark.parametrize("rows,cols,dtype", [(1, 16, torch.bfloat16), (37, 1536, torch.bfloat16),
                                              (6032, 1536, torch.bfloat16), (100, 8960, torch.bfloat16),
                                              (1536, 1536, torch.float32), (3, 2064, torch.float32),
-                                             (9, 4112, torch.bfloat16), (20, 12288, torch.float32),
+                                             (9, 4112, torch.bfloat16), (2048, 4096, torch.bfloat16),
+                                             (2049, 16, torch.bfloat16), (2050, 2064, torch.float32),
+                                             (3000, 1024, torch.float32), (20, 12288, torch.float32),
                                              (64, 16400, torch.bfloat16)])
 def test_quant_rows_bit_exact(rows, cols, dtype):
     g = torch.Generator().manual_seed(rows + cols)
@@ -202,6 +204,13 @@ def test_quant_nonfinite_rows():
         assert _nan_equal(m8.view(torch.uint8)[:6].cpu(), mb)
         assert torch.equal(me.view(torch.uint8)[:6].cpu(), mer)
         assert int(x8.view(torch.uint8)[2, 4].cpu()) == 0x80 and (mer[2, 0] == 255) and (mer[2, 1:] != 255).all()
+        # the same rows among 2048 others: the one-wave-per-row kernel of calls with many rows
+        big = torch.cat([x, torch.randn(2048, 1536, generator=g).to(dtype)])
+        b8, bs = _k().quant_rows_fp8(big.to(DEV))
+        torch.cuda.synchronize()
+        rb, rs = fp8.quant_rows(big)
+        assert _nan_equal(b8.view(torch.uint8).cpu(), rb)
+        assert torch.equal(bs.cpu().isnan(), rs.isnan()) and torch.equal(bs.cpu()[~rs.isnan()], rs[~rs.isnan()])
 
 
 def test_mxfp8_linear_k_not_a_multiple_of_128():
