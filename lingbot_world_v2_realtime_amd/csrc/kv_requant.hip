@@ -68,9 +68,10 @@ __device__ __forceinline__ void vblock_max(const v4i* vw, float (&vf)[4][8], VBl
   }
 }
 
-// Step 2: thread t forms the scale of table byte t (kept in LDS until step 4 stores the table) (group t >> 7, channel 32 (t & 3) + ((t >> 2) & 31)): the
-// power of two 2^e with amax / 2^e in (224, 448]. amax = f * 2^x with f in [0.5, 1) (a normal float after the
-// floor): e = x - 9 when f <= 0.875 (mantissa bits <= 0x600000), else x - 8; x = biased exponent - 126.
+// Step 2: thread t forms the scale of table byte t (group t >> 7, channel 32 (t & 3) + ((t >> 2) & 31)), kept in
+// LDS until step 4 stores the table: the power of two 2^e with amax / 2^e in (224, 448]. amax = f * 2^x with f in
+// [0.5, 1) (a normal float after the floor): e = x - 9 when f <= 0.875 (mantissa bits <= 0x600000), else x - 8;
+// x = biased exponent - 126.
 __device__ __forceinline__ void vblock_scale(VBlockLds& s) {
   const int t = threadIdx.x, g = t >> 7, ch = 32 * (t & 3) + ((t >> 2) & 31);
   float mx = fmaxf(s.gmax[2 * g][ch], s.gmax[2 * g + 1][ch]);   // the group's two waves
