@@ -41,7 +41,8 @@ def _dropin_buffers(b, h, lk, device):
 
 def sage_attention(q, k, v, tensor_layout="NHD", is_causal=False, sm_scale=None):
     """Quantized attention, the call `sageattn(q, k, v, tensor_layout, is_causal, sm_scale)` makes on sm_120
-    (per-warp int8 Q, mean-smoothed per-block int8 K, per-channel fp8 V; lingbot/layers/attention.py:34-35).
+    (per-warp int8 Q, mean-smoothed per-block int8 K, fp8 V; lingbot/layers/attention.py:34-35), here with V's
+    power-of-two scales per 64-key block, 32-key half and channel.
 
     q [B, Lq, H, 128], k/v [B, Lk, H, 128] for "NHD" ([B, H, L, 128] for "HND"), bf16 or fp16 (quantised from
     their own format) on the GPU. Returns bf16 in q's layout. The K mean and V scales are taken over all Lk keys

@@ -4,8 +4,8 @@ The reference prototyped a cache that keeps K as int8 (frozen mean, per-64-token
 to the bf16 window, re-quantising it on a chunk's first forward and attending with only Q quantised per call
 (experiments/modules/sage_kvq.py:38-111). Here the memory is a ring of chunk slots per layer: each chunk is
 quantised once, with its own mean and V scales, when its K/V are written, and attention runs over the
-current chunk plus the cached ones in one kernel (the per-chunk mean enters as a logit bias q . mean_c, the
-per-chunk V scale as a rescale of the accumulator between chunks).
+current chunk plus the cached ones in one kernel (the per-chunk mean enters as a logit bias q . mean_c; V's
+scales are per 64-key block and the matrix cores apply them, so nothing is rescaled between chunks).
 
 Slot bookkeeping is host integers only (as lingbot/layers/kv_cache.py:1-6 keeps its window positions), so a
 forward can be captured in a HIP graph. Two ways to choose what a forward attends to:
