@@ -69,15 +69,24 @@ def attention_ops(lq, lk, h=H, d=D, b=1):
     return 4.0 * b * h * lq * lk * d
 
 
-def requant_bytes(n, h=H, d=D, v_planes=1, v_table=False):
+def requant_bytes(n, h=H, d=D, v_planes=1):
     """Bytes of one chunk's K/V re-quant: bf16 K and V read once; int8 K and `v_planes` e4m3 V planes written
     once; one fp32 scale per 64-token K block; fp32 mean and V scale per (head, channel). With one V plane this
-    is the algorithmic count (55,607,760 B per layer at 6032 tokens x 12 heads); the second (residual) plane
-    this build also writes is overhead on top of it, and so is its V scale table (v_table: 256 B per 64-token
-    block and head in place of the per-channel fp32 V scale)."""
+    is the algorithmic count (55,607,760 B per layer at 6032 tokens x 12 heads)."""
     nb = (n + 63) // 64
-    v_scale = nb * h * 256 if v_table else h * d * 4
-    return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + h * d * 4 + v_scale
+    return 2 * n * h * d * 2 + (1 + v_planes) * n * h * d + nb * h * 4 + 2 * h * d * 4
+
+
+def requant_moved_bytes(n, h=H, d=D):
+    """Bytes the re-quant's three passes move per layer, as built: bf16 K read twice (statistics, then the
+    quantiser: its mean is a reduction over the whole chunk) and V once; int8 K, both e4m3 V planes and the scale
+    table of every 64-token block written; the K scales and mean; the fp32 K column sums of each 32-token
+    half-block written and read back by the finaliser. 86.2 MB per layer at 6032 tokens x 12 heads, the 2.59 GB
+    per 30 layers that FETCH_SIZE / WRITE_SIZE count (profiles/hbm_traffic_per_call.md)."""
+    nb = (n + 63) // 64
+    kv = n * h * d * 2
+    return (2 * kv + kv + nb * 64 * h * d + 2 * nb * 64 * h * d + nb * h * 256 + nb * h * 4 + h * d * 4 +
+            2 * nb * 2 * h * d * 4)
 
 
 def _profile(name):
@@ -563,7 +572,7 @@ def main():
         rq.write_layers(kl, vl)
     rq_ms = _timed(lambda: rq.write_layers(kl, vl), 10, stream)
     rq_bytes = LAYERS * requant_bytes(CHUNK, H, D)
-    rq_moved = LAYERS * requant_bytes(CHUNK, H, D, v_planes=2, v_table=True)
+    rq_moved = LAYERS * requant_moved_bytes(CHUNK, H, D)
     rq_gbps = rq_bytes / (rq_ms * 1e-3) / 1e9
     del kl, vl, rq
 
@@ -592,7 +601,10 @@ def main():
                      "ops_per_launch": ops, "build_sha16": build},
         "requant": {"layers": LAYERS, "ms": round(rq_ms, 4), "algorithmic_bytes": rq_bytes,
                     "GB/s": round(rq_gbps, 1), "frac_hbm": round(rq_gbps / HBM_PEAK_GBPS, 4),
-                    "bytes_moved_two_v_planes": rq_moved},
+                    "bytes_moved": rq_moved, "GB/s_moved": round(rq_moved / (rq_ms * 1e-3) / 1e9, 1),
+                    "frac_hbm_moved": round(rq_moved / (rq_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                    "note": "frac_hbm: algorithmic bytes (K, V read once; one V plane written); "
+                            "frac_hbm_moved: the bytes the passes move (K read twice, two V planes, partials)"},
     }
     # traffic and counters come from rocprofv3 runs committed in profiles/; they count only when those runs
     # measured this very build (same source fingerprint), and the line says which build they are from

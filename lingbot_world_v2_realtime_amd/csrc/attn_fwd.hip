@@ -106,7 +106,7 @@ struct Piece {      // online-softmax state of one wave after a range of key blo
 // one 1 KB piece of each tile of block j + LEAD into LDS with direct global -> LDS loads, through NSTAGE stages;
 // group A waits for its pieces at the end of a softmax phase, group B at the end of an MFMA phase (in the fast
 // form of the pass both groups wait at both points), so each block has landed before the barrier that opens its
-// first MFMA phase. Stage layout (24 KB, and the block's 256-byte V scale table in a table of its own):
+// first MFMA phase. Stage layout (24 KB; the block's scales go to records of their own, below):
 // K tile 64 rows x 128 B, V tile 128 channels x 64 B, V residual tile; 16-byte chunks XOR-swizzled by row
 // (K: chunk ^ ((row >> 1) & 7), V: chunk ^ ((row >> 2) & 3)) so that the fragment reads of the MFMA operands hit
 // 16 distinct bank groups per 16 lanes, and every 1 KB of a tile is one contiguous DMA of 64 lanes x 16 B.
