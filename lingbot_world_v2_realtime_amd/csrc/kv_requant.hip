@@ -99,9 +99,10 @@ __device__ __forceinline__ void vblock_quant(const float (&vf)[4][8], bool two, 
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int c = 0; c < 8; c += 2) {
-      // |V| * 2^-e <= 448 by the choice of e, and the product is exact (a power-of-two factor)
-      const float y0 = fminf(fmaxf(__fmul_rn(vf[j][c], rec[c]), -V_MAX), V_MAX);
-      const float y1 = fminf(fmaxf(__fmul_rn(vf[j][c + 1], rec[c + 1]), -V_MAX), V_MAX);
+      // |V| * 2^-e <= 448 by the choice of e, and the product is exact (a power-of-two factor), so no clamp: a NaN
+      // or an infinity becomes an e4m3 NaN (as the reference's per-channel quantiser makes its channel NaN)
+      const float y0 = __fmul_rn(vf[j][c], rec[c]);
+      const float y1 = __fmul_rn(vf[j][c + 1], rec[c + 1]);
       const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
       vb[c] |= ((uint32_t)pk & 0xFFu) << (8 * j);
       vb[c + 1] |= (((uint32_t)pk >> 8) & 0xFFu) << (8 * j);

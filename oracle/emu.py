@@ -93,6 +93,13 @@ def e4m3_encode(x):
     return x.clamp(-V_MAX, V_MAX).to(torch.float8_e4m3fn).view(torch.uint8)
 
 
+def e4m3_encode_nonfinite(x):
+    """e4m3_encode for values within e4m3's range, a NaN or an infinity as the NaN code 0x7F (with its sign bit)."""
+    bad = ~torch.isfinite(x)
+    bits = e4m3_encode(torch.where(bad, torch.zeros_like(x), x))
+    return torch.where(bad, (torch.signbit(x).to(torch.uint8) << 7) | 0x7F, bits)
+
+
 def e4m3_decode(bits):
     """e4m3fn bits (uint8) -> fp32."""
     return bits.view(torch.float8_e4m3fn).to(torch.float32)
@@ -173,17 +180,19 @@ def v_group_exponents(v):
     """v [L, H, D] -> e int64 [H, nb, 2, D]: per 64-key block, key group g and channel, the exponent of the power of
     two 2^e with amax / 2^e in (224, 448], amax over the group's 32 keys (padding tokens count as zero; floored at
     1e-7). With amax = f * 2^x, f in [0.5, 1): e = x - 9 when f <= 0.875 (448 = 0.875 * 2^9), else x - 8 -- integer
-    arithmetic on the exponent, no rounding."""
+    arithmetic on the exponent, no rounding. A NaN does not enter the amax (the kernel's max skips it); an infinite
+    amax takes the kernel's bit rule for the exponent field 255, x = 129: e = 120."""
     v = _as_lhd(v)
     n, h, d = v.shape
     lp = pad_to(n, K_BLOCK)
     x = torch.zeros(h, lp, d, dtype=torch.float32)
-    x[:, :n] = v.float().abs().permute(1, 0, 2)
+    x[:, :n] = v.float().abs().nan_to_num(nan=0.0, posinf=float("inf")).permute(1, 0, 2)
     x = x.view(h, lp // K_BLOCK, K_BLOCK, d)
     grp = torch.from_numpy(V_GROUP_OF_KEY)
     amax = torch.stack([x[:, :, grp == g].amax(dim=2) for g in (0, 1)], dim=2).clamp_min(AMAX_FLOOR)
     f, ex = torch.frexp(amax)
-    return torch.where(f <= 0.875, ex - 9, ex - 8).long()
+    e = torch.where(f <= 0.875, ex - 9, ex - 8).long()
+    return torch.where(amax.isinf(), torch.full_like(e, 120), e)
 
 
 def v_scale_table(e):
@@ -218,9 +227,9 @@ def quant_v(v):
     recip = torch.ldexp(torch.ones(per_key.shape), -per_key).view(h, lp, d)
     y = torch.zeros(h, lp, d, dtype=torch.float32)
     y[:, :n] = v.float().permute(1, 0, 2)
-    y = (y * recip).clamp(-V_MAX, V_MAX)
-    hi = e4m3_encode(y)
-    lo = e4m3_encode((y - e4m3_decode(hi)) * V_LO_SCALE)
+    y = y * recip                                   # |y| <= 448 for finite V: no clamp, a NaN or inf stays one
+    hi = e4m3_encode_nonfinite(y)
+    lo = e4m3_encode_nonfinite((y - e4m3_decode(hi)) * V_LO_SCALE)
     planes = []
     for bits in (hi, lo):
         bits = bits.view(h, lp // K_BLOCK, K_BLOCK, d)[:, :, torch.from_numpy(V_KEY_OF_POS)]   # [h, b, pos, d]

@@ -47,6 +47,51 @@ def test_requant_bit_exact(n):
     _check_chunk(ring, 0, 1, emu.requant(k, v), n)
 
 
+def _nan_equal(a, b):
+    na, nb = (a & 0x7F) == 0x7F, (b & 0x7F) == 0x7F   # any e4m3 NaN code matches any other
+    return torch.equal(na, nb) and torch.equal(a[~na], b[~nb])
+
+
+def test_requant_nonfinite_v():
+    """A NaN or an infinity in V: the same scale table as the oracle (a NaN does not enter its half-block's amax,
+    an infinity takes it to exponent 120), NaN codes where they are, the other codes bit-exact; the attention is
+    then NaN in the NaN's channel and equal to the oracle's elsewhere."""
+    torch.manual_seed(13)
+    h, n = 2, 130
+    k = (torch.randn(1, n, h, 128) + 2 * torch.randn(1, 1, h, 128)).to(torch.bfloat16)
+    v = torch.randn(1, n, h, 128).to(torch.bfloat16)
+    v[0, 5, 0, 3] = float("nan")
+    v[0, 70, 1, 9] = float("inf")
+    v[0, 100, 1, 20] = -float("inf")
+    ring = _ring(1, h, n)
+    _k().kv_requant(k.to(DEV), v.to(DEV), ring, 0)
+    torch.cuda.synchronize()
+    ref = emu.requant(k, v)
+    nb = (n + 63) // 64
+    assert torch.equal(ring.v_scale[0, 0, :, :nb].cpu(), ref["v_scale"])
+    assert _nan_equal(ring.v8[0, 0, :, :nb].cpu(), ref["v8"]) and _nan_equal(ring.v8lo[0, 0, :, :nb].cpu(), ref["v8lo"])
+    assert torch.equal(ring.k8[0, 0, :, :nb * 64].cpu(), ref["k8"])
+    # the attention over a V with the NaN only
+    v[0, 70, 1, 9] = 1.0
+    v[0, 100, 1, 20] = 1.0
+    _k().kv_requant(k.to(DEV), v.to(DEV), ring, 0)
+    q = torch.randn(1, 300, h, 128).to(torch.bfloat16)
+    q8, qs, _ = _k().quant_q(q.to(DEV))
+    out = torch.empty(1, 300, h, 128, dtype=torch.bfloat16, device=DEV)
+    _k().attn_fwd(q8, qs, None, 1, 300, h, ring, 0, [0], [n], out)
+    torch.cuda.synchronize()
+    o = out[0].float().cpu()
+    want = emu.attention(q, [emu.requant(k, v)], schedule_gx=_lib_gx())
+    assert torch.equal(o.isnan(), want.isnan()) and bool(o[:, 0, 3].isnan().all()) and int(o.isnan().sum()) == 300
+    fin = ~want.isnan()
+    assert (o[fin] - want[fin]).abs().max() < 2e-2
+
+
+def _lib_gx():
+    from lingbot_world_v2_realtime_amd import _lib
+    return _lib.load().lbw_attn_workgroups_per_xcd()
+
+
 @pytest.mark.parametrize("layers,n", [(3, 65536), (1, 262400)])
 def test_requant_long_chunks(layers, n):
     """Long chunks, bit-exact: 65536 tokens (1024 blocks, 256 four-block super-blocks) in 3 layers, and 262400

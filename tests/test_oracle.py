@@ -201,6 +201,38 @@ def test_v_groups_and_scale_table_layout():
     assert torch.equal(emu.v_exponents_of_table(t), e)
 
 
+def test_v_nonfinite_values():
+    """A NaN does not enter its group's amax, so the group's other values get the same codes as with a 0 in its
+    place, and it becomes a NaN code; an infinity takes its group to exponent 120 (the kernel's bit rule), where its
+    finite values underflow to 0 and it becomes a NaN code; the attention output is then NaN in that channel only
+    (as the reference's per-channel scale makes the whole channel NaN)."""
+    torch.manual_seed(12)
+    v = torch.randn(128, 2, 128).to(torch.bfloat16)
+    clean = v.clone()
+    v[5, 0, 3] = float("nan")
+    clean[5, 0, 3] = 0
+    v[70, 1, 9] = float("inf")
+    a8, alo, at = emu.quant_v(v)
+    c8, clo, ct = emu.quant_v(clean)
+    pos = int(emu.V_POS_OF_KEY[5])
+    nan = (a8 & 0x7F) == 0x7F
+    assert bool(nan[0, 0, 3, pos]) and int(nan.sum()) == 2 and bool(nan[1, 1, 9, int(emu.V_POS_OF_KEY[6])])
+    keep = torch.ones_like(nan)
+    keep[1, 1, 9] = False                              # the infinite value's block and channel
+    assert torch.equal(a8[keep & ~nan], c8[keep & ~nan]) and torch.equal(alo[keep & ~nan], clo[keep & ~nan])
+    e = emu.v_exponents_of_table(at)
+    assert int(e[1, 1, 0, 9]) == 120 and int(emu.v_exponents_of_table(ct)[1, 1, 0, 9]) != 120
+    grp0 = torch.tensor([int(emu.V_POS_OF_KEY[k]) for k in range(32)])   # the infinity's half: keys 0-31
+    codes = a8[1, 1, 9, grp0]
+    assert int(((codes & 0x7F) == 0x7F).sum()) == 1 and int(((codes & 0x7F) != 0).sum()) == 1   # else +-0
+    # through the attention: channel 3 of head 0 is NaN for every query, the rest finite
+    q, k, _, _ = emu.make_inputs(40, 128, h=2, seed=3)
+    v2 = v.clone()
+    v2[70, 1, 9] = 1.0
+    out = emu.attention(q, [emu.requant(k, v2)])
+    assert bool(out[:, 0, 3].isnan().all()) and int(out.isnan().sum()) == 40
+
+
 def test_v_position_map_is_a_bijection():
     assert sorted(emu.V_KEY_OF_POS.tolist()) == list(range(64))
     assert np.array_equal(emu.V_POS_OF_KEY[emu.V_KEY_OF_POS], np.arange(64))
