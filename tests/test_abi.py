@@ -88,6 +88,7 @@ def test_requant_argument_checks(lib):
     assert requant(lib, ks=(0, 0, 256, 129)) == E_ALIGN
     assert requant(lib, k8=FAKE + 8) == E_ALIGN
     assert requant(lib, v8lo=FAKE + 4) == E_ALIGN
+    assert requant(lib, v_scale=FAKE + 2) == E_ALIGN  # the V scale table is stored as dwords
     assert requant(lib, dtype=2) == E_SHAPE            # bf16 (0) or fp16 (1) only
 
 
@@ -158,6 +159,7 @@ def test_norm_rope_argument_checks(lib):
     assert norm_rope_kv(lib, slot=4) == E_SHAPE
     assert norm_rope_kv(lib, vs=(0, 256, 12)) == E_ALIGN
     assert norm_rope_kv(lib, k8=FAKE + 8) == E_ALIGN
+    assert norm_rope_kv(lib, v_scale=FAKE + 1) == E_ALIGN
 
 
 def cross(lib, **kw):
@@ -237,6 +239,7 @@ def test_attn_argument_checks(lib):
     assert attn(lib, os=(0, 256, 130)) == E_ALIGN
     assert attn(lib, out=FAKE + 2) == E_ALIGN
     assert attn(lib, v8=FAKE + 8) == E_ALIGN
+    assert attn(lib, vs=FAKE + 2) == E_ALIGN              # the V scale table is read as dwords
     # first tokens: a chunk read from token `first` must end inside its slot
     first = lambda *f: (ctypes.c_int32 * 8)(*f, *[0] * (8 - len(f)))  # noqa: E731
     assert attn(lib, first=first(0, 0, 0, 29)) == E_SEGMENTS          # 29 + 100 > 128
