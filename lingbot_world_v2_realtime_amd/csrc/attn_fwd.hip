@@ -2,9 +2,10 @@
 // domain, e4m3 P times e4m3 V on v_mfma_f32_32x32x64_f8f6f4, fp32 accumulation.
 //
 // Tile: 8 waves x 32 queries = 256 queries of one batch*head. Each wave computes S^T = K Q^T (keys on the MFMA
-// M axis, queries on N), so a lane holds one query and 16 keys of each 32x32 S tile: the row max and row sum
-// are in-lane plus one exchange with lane ^ 32 (v_permlane32_swap), and the S tile's register layout is directly
-// the B operand (P^T) of the PV product O^T = V^T P^T because the fp8 V block stores its keys in that order.
+// M axis, queries on N), so a lane holds one query and 16 keys of each 32x32 S tile: the row max is in-lane
+// plus one exchange with lane ^ 32 (v_permlane32_swap), and the S tile's register layout is directly the B
+// operand (P^T) of the PV product O^T = V^T P^T because the fp8 V block stores its keys in that order. The row
+// sum of the rounded P is one more matrix product per block (a ones operand times the same P^T).
 // The int32 accumulator starts at the bits of 1 / (2 pi) (an inline constant of the MFMA), so its result reads
 // directly as the float 1/(2 pi) + S * 2^-26 (|S| <= 2^21, one binade): the int -> float conversion is free, and
 // the logit scale carries the factor 2^26. The two 4-wave halves of the workgroup run
@@ -61,14 +62,10 @@ constexpr int S_MASKED = (int)0xFF800000;      // bits of -inf: the int max igno
 constexpr int E8M0_ONE = 0x7F7F7F7F;           // MFMA block scale 1.0 in every byte
 constexpr int E8M0_LO = 0x7B7B7B7B;            // 2^-4: the lo plane carries (y - hi) * 16
 
-// max / sum of a value over the two lane halves (lanes l and l ^ 32 hold the same query)
+// max of a value over the two lane halves (lanes l and l ^ 32 hold the same query)
 __device__ __forceinline__ int halves_max_i(int x) {
   auto r = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
   return max((int)r[0], (int)r[1]);
-}
-__device__ __forceinline__ float halves_sum(float x) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // max of 32 ints as a tree of 3-input maxes (v_max3_i32)
@@ -82,20 +79,23 @@ __device__ __forceinline__ int max32i(const int* f) {
   return max(max(b0, b1), max(b2, b3));
 }
 
-__device__ __forceinline__ float sum32(const float* p) {
-  float s[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = p[2 * i] + p[2 * i + 1];
-#pragma unroll
-  for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-    for (int i = 0; i < w; ++i) s[i] = s[2 * i] + s[2 * i + 1];
-  return s[0];
+// Row sums on the matrix core: one v_mfma_scale_f32_16x16x128_f8f6f4 per block multiplies a ones operand with the
+// packed P^T (the 32 x 32 x 64 B operand of the P V products, read as the 16 x 16 x 128 B operand). There, lane l
+// holds column l % 16 and lane group l / 16 of K; the groups hold queries 0-15 / 16-31 (key half 0) and 0-15 /
+// 16-31 (key half 1). A row m takes ones from groups {0, 2} when m & 4 == 0 and from groups {1, 3} otherwise, so
+// the four rows 4 (l / 16) .. + 3 that lane l receives all hold the full key sum of the lane's own query l % 32.
+// The ones are e4m3 (0x38): the operand must have P's format, whose K order within a lane it then shares.
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int E4M3_ONES = 0x38383838;
+__device__ __forceinline__ v8i rowsum_ones(int lane) {
+  const int o = (((lane & 4) != 0) == (((lane >> 4) & 1) != 0)) ? E4M3_ONES : 0;
+  const v8i r = {o, o, o, o, o, o, o, o};
+  return r;
 }
 
 struct Piece {      // online-softmax state of one wave after a range of key blocks
   v16f o[4];        // O^T accumulator, in true V units (the PV MFMAs apply V's block scales)
-  float m, l;       // reference max (log2 domain, bias included) and row sum (both lane halves combined)
+  float m, l;       // reference max (log2 domain, bias included) and row sum of the rounded P
 };
 
 // ---- 8-wave ping-pong attention --------------------------------------------------------------------------
@@ -247,7 +247,9 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) st.o[mt][i] = 0.f;
-  float m_ref = -INFINITY, l_run = 0.f;
+  float m_ref = -INFINITY;
+  v4f l_run = {0.f, 0.f, 0.f, 0.f};      // row sum of the rounded P (all four words equal)
+  const v8i ones = rowsum_ones(lane);
   const bool multi = a.n_seg > 1;
 
   // fragment read offsets in a stage (K: chunk 4g + kk of row 32 mt + lq; V: chunks 2g, 2g + 1 of row 32 mt + lq)
@@ -462,7 +464,10 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
           vq[1] = nx[1];
         }
       }
-      asm volatile("" : "+v"(st.o[0]), "+v"(st.o[1]), "+v"(st.o[2]), "+v"(st.o[3]));   // as for acc
+      // the row sums of block it - 1's rounded P, after the P V products (at the phase start, ahead of the QK
+      // products, it delayed them: the matrix core would not start the first QK product any earlier)
+      l_run = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ones, pb, l_run, 0, 0, 0, E8M0_ONE, 0, E8M0_ONE);
+      asm volatile("" : "+v"(st.o[0]), "+v"(st.o[1]), "+v"(st.o[2]), "+v"(st.o[3]), "+v"(l_run));   // as for acc
     }
     if (!FAST && it == n) return true;
     // B's pieces of block it + 1 have landed before A starts on it (it + 2 .. it + LEAD in flight). The fast
@@ -518,7 +523,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     if (__builtin_expect(__any(moved), 0)) {   // wave-uniform and rare
       const float m_new = moved ? m_blk : m_ref;
       const float alpha = __builtin_amdgcn_exp2f(m_ref - m_new);
-      l_run *= alpha;
+      l_run *= alpha;   // the row sums through block it - 1, like O
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -531,7 +536,6 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     float p[32];
 #pragma unroll
     for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(si[i]), cb, kc));
-    l_run += sum32(p);
     // P^T B operand: byte 16 mt' + 4 i + j of this lane = p[16 mt' + 4 i + j] (keys 32 mt' + 8 i + 4 g + j).
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
@@ -579,7 +583,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   if (grp_a) phase_barrier();   // matches group B's extra barrier at the start
   phase_barrier();               // every wave is done with the stages before they are refilled
   st.m = m_ref;
-  st.l = halves_sum(l_run);
+  st.l = l_run[0];
 }
 
 // Whole tile: O = o / l as bf16; lane (query lq) writes channels 32 mt + 8 i + 4 g + (0..3).

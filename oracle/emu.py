@@ -319,8 +319,9 @@ def attn_schedule(n_tiles, nb, gx):
 def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=None, p_round=True):
     """Online softmax over tile-relative key blocks [j0, j1) (numbered across the chunks in order) for the
     query rows `qf` (q8 as fp32) -> (o in true V units, m, l). The reference max m of a row moves only when a
-    block's max exceeds it by more than `tau`. With p_round=False, P enters the PV product unrounded (fp32)
-    instead of as e4m3."""
+    block's max exceeds it by more than `tau`. The row sum l adds up the P that the PV product multiplies: the e4m3
+    P (so O / l normalises exactly the weights applied to V), or with p_round=False the unrounded fp32 P. The
+    reference's Sage kernel sums the unrounded P instead (a deviation of ~2^-5 / sqrt(keys) relative in l)."""
     rows, d = qf.shape[0], qf.shape[1]
     m_run = torch.full((rows,), float("-inf"))
     l_run = torch.zeros(rows)
@@ -348,8 +349,8 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
             kc = (beta - m_new + (P_OFFSET - tau)).double()
             x = (s_int.double() * cb.double()[:, None] + kc[:, None]).float()
             p = torch.exp2(x)
-            l_run = l_run + p.sum(dim=1)
             pr = e4m3_decode(e4m3_encode(p)) if p_round else p
+            l_run = l_run + pr.sum(dim=1)
             # V in true units: its group scales are powers of two, exact, the factors the MFMA's block scale applies
             o = o + torch.matmul(pr, vdec[ci][hh, k0:k1])
         j += nbc

@@ -287,6 +287,25 @@ def test_attention_small_vs_oracle(lq, lk):
     assert err_sdpa.mean() <= 1.1 * err_scheme.mean() + 1e-5
 
 
+def test_attention_row_sum_of_rounded_p():
+    """V the same in every key row: the output is that row whatever the logits, because the row sum (a matrix
+    product of ones with the packed P) adds up exactly the rounded P that the P V products apply. So the bf16
+    output equals the bf16 rounding of the dequantised row almost everywhere; a row sum of the unrounded P would
+    scale it by sum(e4m3(P)) / sum(P) (1e-3 to 1e-2 away from 1) and move a large share of the values."""
+    torch.manual_seed(43)
+    h, n, lq = 3, 1000, 300
+    q = torch.randn(1, lq, h, 128).to(torch.bfloat16)
+    k = (torch.randn(1, n, h, 128) * 2).to(torch.bfloat16)
+    v = torch.randn(1, 1, h, 128).expand(1, n, h, 128).to(torch.bfloat16).contiguous()
+    out = _attn_gpu(q, k, v)[0]
+    vrow = emu.dequant_v(emu.requant(k, v))[:, 0]                       # [h, 128], fp32
+    want = vrow.to(torch.bfloat16).float()[None].expand(lq, -1, -1)
+    same = (out == want).float().mean().item()
+    print(f"bf16-identical share {same:.5f}, max rel {((out - want).abs() / want.abs()).max():.3e}")
+    assert same >= 0.99
+    assert ((out - want).abs() <= 2 ** -8 * want.abs()).all()
+
+
 @pytest.mark.parametrize("lk", [65000, 66000])
 def test_attention_long_window(lk):
     """One chunk of 65000 / 66000 keys (1016 / 1032 key blocks, over a thousand passes of the block loop per tile)

@@ -417,6 +417,31 @@ def test_online_split_and_chunk_switch_exact_without_p_rounding(gx):
     assert err < 2e-5 * want.abs().max().item(), err
 
 
+def test_row_sum_adds_the_rounded_p():
+    """O / l must normalise exactly the weights the PV product applies. With V the same in every key row (each
+    channel its own value, so every half-block quantises it to the same codes) the output is that row whatever
+    the logits, to fp32 rounding, across chunks, a chunk switch and split tiles. A row sum of the unrounded P
+    would scale the output by sum(e4m3(P)) / sum(P), about 1e-3 away from 1 for such weights, which the bound
+    sees."""
+    g = torch.Generator().manual_seed(41)
+    h, lq = 2, 300
+    q = torch.randn(1, lq, h, 128, generator=g).to(torch.bfloat16)
+    row = torch.randn(1, 1, h, 128, generator=g)
+    chunks = []
+    for i, n in enumerate((200, 333)):
+        k = (torch.randn(1, n, h, 128, generator=g) * (1 + i)).to(torch.bfloat16)
+        chunks.append(emu.requant(k, row.expand(1, n, h, 128).to(torch.bfloat16).contiguous()))
+    vrow = emu.dequant_v(chunks[0])[:, 0]
+    for c in chunks:
+        assert torch.equal(emu.dequant_v(c)[:, :c["n"]], vrow[:, None].expand(-1, c["n"], -1))
+    for gx in (None, 16):
+        got = emu.attention(q, chunks, schedule_gx=gx)
+        assert ((got - vrow[None]).abs() <= 1e-5 * vrow.abs()[None] + 1e-7).all()
+    # the effect a sum of the unrounded weights would have, on weights like these
+    p = torch.exp2(torch.rand(533, generator=g) * 8.8)
+    assert abs(float(emu.e4m3_decode(emu.e4m3_encode(p)).sum() / p.sum()) - 1) > 1e-4
+
+
 @pytest.mark.parametrize("gx", [None, 2, 16])
 def test_windows_read_from_mid_chunk_exact_without_p_rounding(gx):
     """Chunks read over a window of their keys, as the token window reads them: a suffix from a key inside a
