@@ -193,7 +193,8 @@ int lbw_quant_mx_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t rows_pa
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the
  * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA with V's E8M0 block scales applied by
  * the MFMA itself (a second fp8 product with the residual plane, scaled 2^-4 lower, when v8lo is not null), fp32
- * accumulation, 1 / row sum applied at the end. Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
+ * accumulation, 1 / row sum applied at the end (the row sum adds the e4m3 P the products apply, formed on the
+ * matrix core; the reference sums the unrounded P). Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
  * 126-127; experiments/modules/sage_kvq.py:107-110). seg_slot / seg_len are host arrays. `workspace` holds
  * lbw_attn_workspace_bytes() bytes (16-byte aligned); two kernels run: the attention over a persistent grid
  * and a merge of the query tiles whose keys were split between workgroups.
