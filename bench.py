@@ -451,6 +451,25 @@ def fp8_linear_calls(dev, steps=30):
         out[name] = {"ms": round(ms, 4), "default_solution_ms": round(times["default"], 4), "gemm_table": table,
                      "act_quant_call_ms": round(q_ms, 4), "TFLOP/s": round(tf, 1),
                      "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4)}
+    # the feed-forward block's GELU + down projection: torch's GELU then the FP8 linear (two passes over the
+    # 6032 x 8960 activation), against the GELU fused into the activation quantisation (FP8Linear gelu_input,
+    # what convert_to_fp8(fuse_gelu=True) builds); both with the tuned solution table
+    lin = torch.nn.Linear(FFN, DIM).to(torch.bfloat16).to(dev)
+    plain, fused = FP8Linear(lin), FP8Linear(lin, gelu_input=True)
+    h = torch.randn(1, LQ, FFN, device=dev).to(torch.bfloat16)
+    table = use_tuned_gemms()
+    unfused_fn = lambda: plain(torch.nn.functional.gelu(h, approximate="tanh"))   # noqa: E731
+    fused_fn = lambda: fused(h)                                                   # noqa: E731
+    for fn in (unfused_fn, fused_fn):
+        for _ in range(3):
+            fn()
+    torch.cuda.synchronize()
+    t_unfused = _timed(unfused_fn, steps, stream)
+    t_fused = _timed(fused_fn, steps, stream)
+    t_gq = _timed(lambda: kernels.quant_rows_fp8_gelu(h.view(LQ, FFN)), steps, stream)
+    tunable.enable(False)
+    out["ffn_gelu_down_8960x1536"] = {"ms": round(t_fused, 4), "unfused_ms": round(t_unfused, 4),
+                                      "gelu_act_quant_call_ms": round(t_gq, 4), "gemm_table": table}
     # the MXFP8 mode (per-32 E8M0 scales) at the projection shape: its GEMM pads the rows to 128
     from lingbot_world_v2_realtime_amd.layers.linear import MXFP8Linear
     lin = torch.nn.Linear(DIM, DIM).to(torch.bfloat16).to(dev)

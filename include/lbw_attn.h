@@ -175,6 +175,18 @@ int lbw_quant_rows_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t cols,
                        uint8_t* x8, float* scale, void* stream);
 
 /*
+ * The feed-forward activation and the next linear's activation quantisation in one pass: y = GELU(x) in its tanh
+ * form, rounded to bf16 (nn.GELU(approximate='tanh') on bf16 x, the activation between the two linears of
+ * lingbot/models/lingbot_world/transformer.py:313-315), then x8 / scale exactly as lbw_quant_rows_fp8 gives them
+ * for that bf16 y. x bf16 [rows][cols] (row stride s_row elements, cols a multiple of 16). GELU is evaluated as
+ * x / (1 + e^(-2u)) with the hardware exp2 and reciprocal: within a few fp32 ulps of the exact value, so y differs
+ * from the correctly rounded bf16 GELU only for values within that distance of a bf16 rounding boundary. Replaces
+ * the GELU + activation quantisation of lingbot/layers/linear.py:15-26 that a compiled reference fuses.
+ */
+int lbw_quant_rows_fp8_gelu(const uint16_t* x, int64_t rows, int64_t cols, int64_t s_row, uint8_t* x8,
+                            float* scale, void* stream);
+
+/*
  * MXFP8 quantisation of x [rows][cols] (bf16, or fp32 when x_is_fp32; row stride s_row; cols a multiple of 32):
  * per 32 consecutive values, scale = 2^e, e = ceil(log2(max(amax, 2^-126) / 448)) (exact, floored at -127),
  * x8 = e4m3(x / scale) and scale_e8m0 = e + 127, rows packed (x8 [rows_pad][cols], scale_e8m0

@@ -24,6 +24,7 @@ SIGNATURES = {
     "lbw_cross_attn_fwd": (_i32, [_p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64,
                                   _f32, _p]),
     "lbw_quant_rows_fp8": (_i32, [_p, _i32, _i64, _i64, _i64, _p, _p, _p]),
+    "lbw_quant_rows_fp8_gelu": (_i32, [_p, _i64, _i64, _i64, _p, _p, _p]),
     "lbw_quant_mx_fp8": (_i32, [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p]),
     "lbw_attn_fwd": (_i32, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _i64, _i32, _p, _p, _p,
                             _p, _i64, _i64, _i64, _f32, _p, _p]),

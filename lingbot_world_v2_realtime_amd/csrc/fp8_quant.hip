@@ -33,6 +33,30 @@ struct Row8<float> {      // fp32: 8 values = 32 bytes
   }
 };
 
+// GELU in its tanh form (nn.GELU(approximate='tanh'), the feed-forward activation of the DiT blocks,
+// lingbot/models/lingbot_world/transformer.py:313-315): 0.5 x (1 + tanh(u)) with u = sqrt(2 / pi) (x + 0.044715 x^3),
+// evaluated as the identical x / (1 + e^(-2u)) on the hardware exp2 and reciprocal, then rounded to bf16 (the
+// module's output type; round to nearest even). The fp32 value is within a few ulps of the exact one, so the bf16
+// result is the correctly rounded GELU except for values that close to a bf16 rounding boundary. Large negative x:
+// e^(-2u) overflows to inf and the result is -0 (the exact value underflows); +-inf give inf / NaN and a NaN stays
+// NaN, as the tanh form does.
+__device__ __forceinline__ float gelu_tanh_bf16(float x) {
+  constexpr float NEG2_SQRT2PI_LOG2E = -2.f * 0.7978845608028654f * 1.4426950408889634f;
+  const float a = fmaf(0.044715f * x, x, 1.f);                 // 1 + 0.044715 x^2
+  const float e = __builtin_amdgcn_exp2f(NEG2_SQRT2PI_LOG2E * x * a);
+  const float g = x * __builtin_amdgcn_rcpf(1.f + e);
+  return (float)(__bf16)g;
+}
+
+template <bool GELU, typename T>
+__device__ __forceinline__ void load8(const T* p, float* f) {
+  Row8<T>::load(p, f);
+  if constexpr (GELU) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = gelu_tanh_bf16(f[e]);
+  }
+}
+
 // x / sc rounded to nearest, from the row's reciprocal r = RN(1 / sc): q = RN(x r) is within an ulp of x / sc, the
 // remainder x - q sc is exact under an FMA, and RN(q + rem r) is the correctly rounded quotient (Markstein's
 // correction step); the sign comes from x, so a zero quotient keeps it. Equal to IEEE division wherever
@@ -97,7 +121,7 @@ __device__ __forceinline__ float row_scale(uint32_t amax_bits, uint32_t* s_red, 
 
 // Rows of at most NCH * 512 values, a one-wave workgroup each: lane l holds 8-value chunks l, l + 64, ... in
 // registers. The same amax, scale and quotients as the workgroup-per-row kernels.
-template <typename T, int NCH>
+template <typename T, int NCH, bool GELU>
 __global__ __launch_bounds__(64) void quant_rows_fp8_wave_kernel(const T* __restrict__ x, int64_t cols, int64_t s_row,
                                                                  uint8_t* __restrict__ x8, float* __restrict__ scale) {
   const int64_t row = blockIdx.x;
@@ -109,7 +133,7 @@ __global__ __launch_bounds__(64) void quant_rows_fp8_wave_kernel(const T* __rest
   for (int i = 0; i < NCH; ++i) {
     const int64_t c = 8 * (int64_t)(lane + 64 * i);
     if (c < cols) {
-      Row8<T>::load(xr + c, f[i]);
+      load8<GELU>(xr + c, f[i]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[i][e] = 0.f;
@@ -130,7 +154,7 @@ __global__ __launch_bounds__(64) void quant_rows_fp8_wave_kernel(const T* __rest
 }
 
 // Rows of at most NCH * 2048 values: thread t holds 8-value chunks t, t + 256, ... in registers.
-template <typename T, int NCH>
+template <typename T, int NCH, bool GELU>
 __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict__ x, int64_t cols, int64_t s_row,
                                                              uint8_t* __restrict__ x8, float* __restrict__ scale) {
   __shared__ uint32_t s_red[4];
@@ -143,7 +167,7 @@ __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict
   for (int i = 0; i < NCH; ++i) {
     const int64_t c = 8 * (int64_t)(t + 256 * i);
     if (c < cols) {
-      Row8<T>::load(xr + c, f[i]);
+      load8<GELU>(xr + c, f[i]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[i][e] = 0.f;
@@ -162,7 +186,7 @@ __global__ __launch_bounds__(256) void quant_rows_fp8_kernel(const T* __restrict
 }
 
 // Longer rows: the amax pass and the quantise pass each read the row.
-template <typename T>
+template <typename T, bool GELU>
 __global__ __launch_bounds__(256) void quant_rows_fp8_long_kernel(const T* __restrict__ x, int64_t cols,
                                                                   int64_t s_row, uint8_t* __restrict__ x8,
                                                                   float* __restrict__ scale) {
@@ -173,7 +197,7 @@ __global__ __launch_bounds__(256) void quant_rows_fp8_long_kernel(const T* __res
   uint32_t amax = 0;
   for (int64_t c = 8 * (int64_t)t; c < cols; c += 8 * 256) {
     float f[8];
-    Row8<T>::load(xr + c, f);
+    load8<GELU>(xr + c, f);
 #pragma unroll
     for (int e = 0; e < 8; ++e) amax = max(amax, abs_bits(f[e]));
   }
@@ -182,12 +206,12 @@ __global__ __launch_bounds__(256) void quant_rows_fp8_long_kernel(const T* __res
   uint8_t* outr = x8 + row * cols;
   for (int64_t c = 8 * (int64_t)t; c < cols; c += 8 * 256) {
     float f[8];
-    Row8<T>::load(xr + c, f);
+    load8<GELU>(xr + c, f);
     *(uint2*)(outr + c) = quant8(f, sc, r);
   }
 }
 
-template <typename T>
+template <typename T, bool GELU>
 static void launch_quant_rows(const T* x, int64_t rows, int64_t cols, int64_t s_row, uint8_t* x8, float* scale,
                               hipStream_t stream) {
   const dim3 grid((unsigned)rows), block(256);
@@ -195,30 +219,30 @@ static void launch_quant_rows(const T* x, int64_t rows, int64_t cols, int64_t s_
     const dim3 wblock(64);
     const int64_t wch = (cols + 511) / 512;
     if (wch <= 1)
-      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 1>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 1, GELU>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
     else if (wch <= 2)
-      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 2>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 2, GELU>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
     else if (wch <= 3)
-      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 3>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 3, GELU>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
     else if (wch <= 4)
-      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 4>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 4, GELU>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
     else
-      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 8>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
+      hipLaunchKernelGGL((quant_rows_fp8_wave_kernel<T, 8, GELU>), grid, wblock, 0, stream, x, cols, s_row, x8, scale);
     return;
   }
   const int64_t nch = (cols + 2047) / 2048;
   if (nch <= 1)
-    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 1>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 1, GELU>), grid, block, 0, stream, x, cols, s_row, x8, scale);
   else if (nch <= 2)
-    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 2>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 2, GELU>), grid, block, 0, stream, x, cols, s_row, x8, scale);
   else if (nch <= 4)
-    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 4>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 4, GELU>), grid, block, 0, stream, x, cols, s_row, x8, scale);
   else if (nch <= 5)
-    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 5>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 5, GELU>), grid, block, 0, stream, x, cols, s_row, x8, scale);
   else if (nch <= 8)
-    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 8>), grid, block, 0, stream, x, cols, s_row, x8, scale);
+    hipLaunchKernelGGL((quant_rows_fp8_kernel<T, 8, GELU>), grid, block, 0, stream, x, cols, s_row, x8, scale);
   else
-    hipLaunchKernelGGL(quant_rows_fp8_long_kernel<T>, grid, block, 0, stream, x, cols, s_row, x8, scale);
+    hipLaunchKernelGGL((quant_rows_fp8_long_kernel<T, GELU>), grid, block, 0, stream, x, cols, s_row, x8, scale);
 }
 
 // MXFP8 (the reference's MXFP8Linear, lingbot/layers/linear.py:42-50): per 32 consecutive values of a row,
@@ -295,9 +319,21 @@ extern "C" int lbw_quant_rows_fp8(const void* x, int x_is_fp32, int64_t rows, in
   if (s_row % 8 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)x8 & 7)) return LBW_E_ALIGN;
   if (const int dv = check_device()) return dv;
   if (x_is_fp32)
-    launch_quant_rows((const float*)x, rows, cols, s_row, x8, scale, (hipStream_t)stream);
+    launch_quant_rows<float, false>((const float*)x, rows, cols, s_row, x8, scale, (hipStream_t)stream);
   else
-    launch_quant_rows((const uint16_t*)x, rows, cols, s_row, x8, scale, (hipStream_t)stream);
+    launch_quant_rows<uint16_t, false>((const uint16_t*)x, rows, cols, s_row, x8, scale, (hipStream_t)stream);
+  if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
+  return LBW_OK;
+}
+
+extern "C" int lbw_quant_rows_fp8_gelu(const uint16_t* x, int64_t rows, int64_t cols, int64_t s_row, uint8_t* x8,
+                                       float* scale, void* stream) {
+  if (!x || !x8 || !scale) return LBW_E_NULL;
+  if (rows <= 0 || cols <= 0 || rows > 0x7fffffff || cols % 16 != 0) return LBW_E_SHAPE;
+  if (s_row < cols) return LBW_E_SHAPE;
+  if (s_row % 8 != 0 || ((uintptr_t)x & 15) || ((uintptr_t)x8 & 7)) return LBW_E_ALIGN;
+  if (const int dv = check_device()) return dv;
+  launch_quant_rows<uint16_t, true>(x, rows, cols, s_row, x8, scale, (hipStream_t)stream);
   if (hipGetLastError() != hipSuccess) return LBW_E_LAUNCH;
   return LBW_OK;
 }

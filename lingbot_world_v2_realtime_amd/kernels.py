@@ -308,6 +308,25 @@ def quant_rows_fp8(x):
     return x8, scale
 
 
+def quant_rows_fp8_gelu(x):
+    """GELU (tanh form, rounded to bf16) of a 2-d bf16 device tensor x [rows, cols], then its rowwise e4m3 as
+    quant_rows_fp8 gives it, in one pass (lbw_quant_rows_fp8_gelu): (x8 float8_e4m3fn [rows, cols], scale fp32
+    [rows, 1]) with gelu(x) ~ x8 * scale."""
+    lib = _lib.load()
+    if not x.is_cuda:
+        raise ValueError("x must be a device tensor (the FP8 path has no CPU implementation)")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"x must be bfloat16, got {x.dtype}")
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError(f"x must be 2-d with contiguous rows, got {tuple(x.shape)} / {x.stride()}")
+    rows, cols = x.shape
+    x8 = torch.empty(rows, cols, dtype=torch.float8_e4m3fn, device=x.device)
+    scale = torch.empty(rows, 1, dtype=torch.float32, device=x.device)
+    st = lib.lbw_quant_rows_fp8_gelu(_ptr(x), rows, cols, x.stride(0), _ptr(x8), _ptr(scale), _stream(x))
+    _lib.check(st, "lbw_quant_rows_fp8_gelu")
+    return x8, scale
+
+
 def quant_mx_fp8(x, rows_pad=None):
     """MXFP8 of a 2-d bf16 / fp32 device tensor x [rows, cols] (cols a multiple of 32, unit column stride):
     (x8 float8_e4m3fn [rows_pad, cols], scale float8_e8m0fnu [rows_pad, cols / 32]), one power-of-two scale per 32

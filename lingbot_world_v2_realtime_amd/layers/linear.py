@@ -58,10 +58,13 @@ def tune_gemms(shapes, path, device="cuda", bias=True):
 
 
 class FP8Linear(torch.nn.Module):
-    """Rowwise FP8 replacement of an nn.Linear (lingbot/layers/linear.py:10-29)."""
+    """Rowwise FP8 replacement of an nn.Linear (lingbot/layers/linear.py:10-29). gelu_input: the module also
+    applies the GELU (tanh form) that precedes it in a feed-forward block, fused into the activation quantisation
+    (lbw_quant_rows_fp8_gelu) for bf16 activations; convert_to_fp8(..., fuse_gelu=True) sets it."""
 
-    def __init__(self, lin):
+    def __init__(self, lin, gelu_input=False):
         super().__init__()
+        self.gelu_input = bool(gelu_input)
         w = lin.weight.detach()
         if w.dtype not in (torch.bfloat16, torch.float32):
             w = w.float()
@@ -74,9 +77,14 @@ class FP8Linear(torch.nn.Module):
     def forward(self, x):
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        if x2.dtype not in (torch.bfloat16, torch.float32):
-            x2 = x2.float()
-        x8, x_scale = kernels.quant_rows_fp8(x2.contiguous())
+        if self.gelu_input and x2.dtype == torch.bfloat16:
+            x8, x_scale = kernels.quant_rows_fp8_gelu(x2.contiguous())
+        else:
+            if self.gelu_input:   # another input type: the GELU in that type first, as the unfused module runs it
+                x2 = torch.nn.functional.gelu(x2, approximate="tanh")
+            if x2.dtype not in (torch.bfloat16, torch.float32):
+                x2 = x2.float()
+            x8, x_scale = kernels.quant_rows_fp8(x2.contiguous())
         y = torch._scaled_mm(x8, self.w8.t(), scale_a=x_scale, scale_b=self.w_scale_t,
                              bias=None if self.bias is None else self.bias.to(torch.bfloat16),
                              out_dtype=torch.bfloat16)
@@ -138,13 +146,24 @@ def fp8_eligible(lin, mx=False):
         lin.in_features % k_mult == 0
 
 
-def convert_to_fp8(blocks, mx=False):
+def convert_to_fp8(blocks, mx=False, fuse_gelu=False):
     """Replace every eligible nn.Linear below `blocks` (fp8_eligible) by FP8Linear, or MXFP8Linear with mx=True,
-    in place. Returns (replaced, linears seen)."""
+    in place. Returns (replaced, linears seen). fuse_gelu (rowwise only): inside an nn.Sequential, a tanh-form
+    nn.GELU directly followed by a replaced linear -- the DiT's feed-forward block,
+    lingbot/models/lingbot_world/transformer.py:313-315 -- becomes nn.Identity and the linear applies the GELU in
+    its activation quantisation (FP8Linear gelu_input), one pass over the activation instead of two."""
     make = MXFP8Linear if mx else FP8Linear
     found = [(path, m) for path, m in blocks.named_modules() if path and isinstance(m, torch.nn.Linear)]
     chosen = [(path, m) for path, m in found if fp8_eligible(m, mx)]
     for path, m in chosen:
         owner, _, attr = path.rpartition(".")
         setattr(blocks.get_submodule(owner), attr, make(m))
+    if fuse_gelu and not mx:
+        for seq in [m for m in blocks.modules() if isinstance(m, torch.nn.Sequential)]:
+            kids = list(seq)
+            for i in range(len(kids) - 1):
+                act, lin = kids[i], kids[i + 1]
+                if isinstance(act, torch.nn.GELU) and act.approximate == "tanh" and isinstance(lin, FP8Linear):
+                    lin.gelu_input = True
+                    seq[i] = torch.nn.Identity()
     return len(chosen), len(found)

@@ -20,6 +20,23 @@ def dequant_rows(bits, scale):
     return bits.view(torch.float8_e4m3fn).float() * scale
 
 
+def gelu_tanh_bf16(x):
+    """nn.GELU(approximate='tanh') of bf16 x, exact then rounded to bf16 (the module's output on bf16 input,
+    lingbot/models/lingbot_world/transformer.py:313-315): 0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))) in
+    fp64, so the result is the correctly rounded bf16 value (torch evaluates it in fp32 and agrees to within a bf16
+    ulp). Non-finite inputs: +inf -> inf, -inf -> NaN (0.5 x (1 + tanh) = -inf * 0), NaN -> NaN."""
+    xd = x.double()
+    inner = (2.0 / torch.pi) ** 0.5 * (xd + 0.044715 * xd * xd * xd)
+    g = 0.5 * xd * (1.0 + torch.tanh(inner))
+    # fp64 -> bf16 rounded once: through fp32 a value can land exactly on a bf16 tie that the fp64 value is not
+    # on; such fp32 values are moved one fp32 ulp toward the fp64 value first, so the tie breaks the right way
+    f = g.float()
+    tie = ((f.view(torch.int32) & 0xFFFF) == 0x8000) & (f.double() != g)
+    toward = torch.where(g > f.double(), torch.tensor(float("inf")), torch.tensor(float("-inf")))
+    f = torch.where(tie, torch.nextafter(f, toward), f)
+    return f.to(torch.bfloat16)
+
+
 def quant_mx(x):
     """MXFP8 (lingbot/layers/linear.py:42-50) with the scale exponent taken exactly: x [rows, cols] bf16 / fp32,
     cols a multiple of 32 -> (e4m3 bits uint8 [rows, cols], E8M0 bytes uint8 [rows, cols / 32]). Per 32 values:

@@ -36,7 +36,7 @@ def lib():
 
 def test_header_declarations_are_bound_and_exported(lib):
     decl = declared_functions()
-    assert len(decl) == 17
+    assert len(decl) == 18
     assert set(decl) == set(_lib.SIGNATURES)
     for name, n in decl.items():
         assert len(_lib.SIGNATURES[name][1]) == n, name
@@ -199,6 +199,14 @@ def test_quant_rows_fp8_argument_checks(lib):
     assert q(x=FAKE + 8) == E_ALIGN
     if hip_device_count() == 0:
         assert q() == E_DEVICE
+    gq = lambda **kw: lib.lbw_quant_rows_fp8_gelu(kw.get("x", FAKE), kw.get("rows", 10), kw.get("cols", 256),  # noqa: E731
+                                                  kw.get("s", 256), kw.get("x8", FAKE), kw.get("sc", FAKE), None)
+    assert gq(sc=None) == E_NULL
+    assert gq(cols=100) == E_SHAPE
+    assert gq(s=128) == E_SHAPE
+    assert gq(x8=FAKE + 4) == E_ALIGN
+    if hip_device_count() == 0:
+        assert gq() == E_DEVICE
     mx = lambda **kw: lib.lbw_quant_mx_fp8(kw.get("x", FAKE), 0, kw.get("rows", 10), kw.get("pad", 128),  # noqa: E731
                                            kw.get("cols", 256), kw.get("s", 256), kw.get("x8", FAKE), FAKE, None)
     assert mx(x=None) == E_NULL

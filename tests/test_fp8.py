@@ -141,6 +141,30 @@ def test_mx_exact_exponent_at_a_boundary():
     assert torch.equal(dq[0], x[0])
 
 
+def test_gelu_tanh_against_torch_and_identities():
+    """The oracle's GELU (tanh form, exact then rounded once to bf16) against torch's own nn.GELU(approximate='tanh')
+    evaluated in fp32 on the CPU: for x >= -2 the same bf16 value for every input; below, torch's 1 + tanh(u)
+    cancels (its values there are off by up to ~1e-7 absolute and
+    reach -0 early), so only the absolute agreement holds -- far below a quantisation step of any row holding
+    values of order one. Independent of both formulas: GELU(x) - GELU(-x) = x, GELU(0) = 0, GELU(x) -> x for large
+    x and -> -0 for large negative x, and the non-finite cases of the tanh form."""
+    g = torch.Generator().manual_seed(12)
+    x = (torch.randn(200000, generator=g) * 4).to(torch.bfloat16)
+    ours = fp8.gelu_tanh_bf16(x).float()
+    theirs = torch.nn.functional.gelu(x.float(), approximate="tanh").to(torch.bfloat16).float()
+    step = torch.ldexp(torch.ones_like(ours), (torch.floor(torch.log2(ours.abs().clamp(min=2.0 ** -126))) - 7).int())
+    near = x.float() >= -2
+    assert torch.equal(ours[near], theirs[near])
+    assert ((ours - theirs).abs() <= torch.maximum(step, torch.tensor(1e-6)))[~near].all()
+    xd = x.double()
+    odd = fp8.gelu_tanh_bf16(x).double() - fp8.gelu_tanh_bf16(-x).double()
+    assert ((odd - xd).abs() <= 2.0 ** -7 * xd.abs() + 2.0 ** -120).all()   # two bf16 roundings
+    special = torch.tensor([0.0, 30.0, -30.0, float("inf"), -float("inf"), float("nan")]).to(torch.bfloat16)
+    r = fp8.gelu_tanh_bf16(special).float()
+    assert r[0] == 0 and r[1] == 30.0 and r[2] == 0 and torch.signbit(r[2])
+    assert r[3] == float("inf") and r[4].isnan() and r[5].isnan()
+
+
 def test_mx_grid_zero_groups_and_error_bound():
     g = torch.Generator().manual_seed(4)
     x = torch.randn(16, 256, generator=g)

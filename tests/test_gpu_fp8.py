@@ -242,3 +242,102 @@ def test_convert_to_fp8_mx_selection():
     blk = torch.nn.Sequential(torch.nn.Linear(1536, 1536), torch.nn.Linear(1040, 1536)).to(torch.bfloat16).to(DEV)
     assert convert_to_fp8(blk, mx=True) == (1, 2)   # 1040 is a multiple of 16, not of 32
     assert isinstance(blk[0], MXFP8Linear) and isinstance(blk[1], torch.nn.Linear)
+
+
+def _e4m3_step(v):
+    """Spacing of e4m3 around |v| (fp32 tensor): 2^(e - 3) in the normal range, 2^-9 below it."""
+    e = torch.floor(torch.log2(v.abs().clamp(min=2.0 ** -6)))
+    return torch.ldexp(torch.ones_like(v), (e - 3).int())
+
+
+@pytest.mark.parametrize("rows,cols", [(333, 1536), (2048, 1536), (64, 8960), (6, 20000), (3, 16)])
+def test_quant_rows_gelu_vs_oracle(rows, cols):
+    """GELU (tanh form, bf16) fused into the rowwise quantisation, every kernel form (one wave per row, a workgroup
+    per row with the row in registers, rows read twice), against the oracle: the exact GELU rounded once to bf16,
+    then the oracle's rowwise quantisation. The kernel's GELU is within a few fp32 ulps of exact, so its bf16 value
+    differs from the oracle's only next to a rounding boundary: the scales agree to a bf16 ulp, nearly every code is
+    identical, and no dequantised value is more than one e4m3 step away."""
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    x = (torch.randn(rows, cols, generator=g) * 3).to(torch.bfloat16)
+    x[0, :8] = torch.tensor([0.0, -0.0, 10.0, -10.0, -100.0, 100.0, 1e-3, -1e-3]).to(torch.bfloat16)
+    x8, sc = _k().quant_rows_fp8_gelu(x.to(DEV))
+    torch.cuda.synchronize()
+    gx = fp8.gelu_tanh_bf16(x)
+    rb, rs = fp8.quant_rows(gx)
+    sc = sc.cpu()
+    assert ((sc - rs).abs() <= 2.0 ** -8 * rs).all()
+    codes = x8.view(torch.uint8).cpu()
+    same = (codes == rb).float().mean().item()
+    got, want = fp8.dequant_rows(codes, sc), fp8.dequant_rows(rb, rs)
+    gap = (got - want).abs()
+    step = torch.maximum(_e4m3_step(codes.view(torch.float8_e4m3fn).float()) * sc,
+                         _e4m3_step(rb.view(torch.float8_e4m3fn).float()) * rs)
+    record(f"quant_rows_gelu {rows}x{cols}: identical codes {same:.5f}, max dequant gap / step "
+           f"{(gap / step).max().item():.3f}")
+    assert same >= 0.99
+    assert (gap <= 1.1 * step).all()
+    # the pinned points: GELU(0) = +-0 stays a zero code, GELU(10) = 10, GELU(-100) = -0
+    assert int(codes[0, 0]) in (0, 0x80) and int(codes[0, 4]) in (0, 0x80)
+    assert abs(float(got[0, 2]) - 10.0) <= float(_e4m3_step(torch.tensor(10.0)) * sc[0])
+
+
+def test_quant_rows_gelu_nonfinite_and_torch_gelu():
+    """Non-finite inputs as the tanh form gives them (+inf -> inf: the row's scale inf; -inf -> NaN and NaN -> NaN:
+    the row NaN), finite rows untouched; and on finite rows the fused pass against torch's own GELU on the device
+    followed by the unfused quantiser (the two-launch path it replaces)."""
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(2054, 1536, generator=g) * 2).to(torch.bfloat16)
+    x[1, 5], x[2, 6], x[3, 7] = float("inf"), -float("inf"), float("nan")
+    x8, sc = _k().quant_rows_fp8_gelu(x.to(DEV))
+    y = torch.nn.functional.gelu(x.to(DEV), approximate="tanh")
+    u8, us = _k().quant_rows_fp8(y)
+    torch.cuda.synchronize()
+    sc, us = sc.cpu(), us.cpu()
+    assert float(sc[1]) == float("inf") and bool(sc[2].isnan()) and bool(sc[3].isnan())
+    rb, rs = fp8.quant_rows(fp8.gelu_tanh_bf16(x))
+    assert _nan_equal(x8.view(torch.uint8)[1:4].cpu(), rb[1:4])
+    fin = torch.ones(x.shape[0], dtype=torch.bool)
+    fin[1:4] = False
+    assert ((sc[fin] - us[fin]).abs() <= 2.0 ** -8 * us[fin]).all()
+    same = (x8.view(torch.uint8).cpu()[fin] == u8.view(torch.uint8).cpu()[fin]).float().mean().item()
+    record(f"quant_rows_gelu vs torch gelu + quant_rows: identical codes {same:.5f}")
+    assert same >= 0.99
+
+
+def test_fp8_linear_fused_gelu_and_convert():
+    """The DiT feed-forward block with fuse_gelu: convert_to_fp8 turns its GELU into nn.Identity and lets the second
+    linear apply it in its activation quantisation; the block's output matches the unfused FP8 block (torch's GELU,
+    then the separate quantisation) to the FP8 linears' own tolerance."""
+    from lingbot_world_v2_realtime_amd.layers.linear import FP8Linear, convert_to_fp8
+    g = torch.Generator().manual_seed(17)
+
+    def ffn():
+        torch.manual_seed(3)
+        f = torch.nn.Sequential(torch.nn.Linear(1536, 8960), torch.nn.GELU(approximate="tanh"),
+                                torch.nn.Linear(8960, 1536), torch.nn.GELU(), torch.nn.Linear(1536, 1536))
+        for m in f:
+            if isinstance(m, torch.nn.Linear):
+                with torch.no_grad():
+                    m.weight.mul_(0.5)
+        return f.to(torch.bfloat16).to(DEV)
+
+    plain, fused = ffn(), ffn()
+    assert convert_to_fp8(plain) == (3, 3)
+    assert convert_to_fp8(fused, fuse_gelu=True) == (3, 3)
+    assert isinstance(fused[1], torch.nn.Identity) and fused[2].gelu_input
+    assert isinstance(fused[3], torch.nn.GELU) and not fused[4].gelu_input   # the erf form is left alone
+    assert not plain[2].gelu_input and isinstance(plain[1], torch.nn.GELU)
+    x = torch.randn(2, 300, 1536, generator=g).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        a, b = plain(x), fused(x)
+    torch.cuda.synchronize()
+    e = (a.float() - b.float()).abs()
+    scale = a.float().abs().max().item()
+    record(f"FFN with fused GELU vs unfused: max {e.max().item():.2e} (|out| max {scale:.2e})")
+    assert e.max().item() <= 2e-2 * scale
+    # an FP8Linear with gelu_input on an fp32 activation takes torch's GELU, then the plain quantisation
+    lin = FP8Linear(torch.nn.Linear(1536, 1536).to(torch.bfloat16).to(DEV), gelu_input=True)
+    xf = torch.randn(64, 1536, generator=g).to(DEV)
+    want = FP8Linear(torch.nn.Linear(1536, 1536).to(torch.bfloat16).to(DEV))
+    want.w8, want.w_scale_t, want.bias = lin.w8, lin.w_scale_t, lin.bias
+    assert torch.equal(lin(xf), want(torch.nn.functional.gelu(xf, approximate="tanh")))
