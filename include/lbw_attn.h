@@ -22,13 +22,17 @@
  *   k_scale fp32  [layers][slots][BH][nb]             amax / 127 of each 64-token block
  *   km      fp32  [layers][slots][BH][128]            per-(head, channel) chunk mean (a bf16 value)
  *   v8      uint8 [layers][slots][BH][nb][128][64]    e4m3 V, per 64-key block: [channel][position]
- *   v8lo    uint8 [layers][slots][BH][nb][128][64]    optional second e4m3 plane: (y - hi) * 16, y = V / 2^e
+ *   v8lo    uint8 [layers][slots][BH][nb][128][48]    optional residual plane: bf6 (OCP e3m2) codes of y - hi,
+ *                                                      y = V / 2^e, hi = e4m3(y); per block [channel][48 bytes]
  *   v_scale uint8 [layers][slots][BH][nb][256]        E8M0 V scales of each 64-key block: one power of two 2^e per
  *                                                      (key group, channel) with amax / 2^e in (224, 448] (amax over
  *                                                      the group's 32 keys, floored at 1e-7), so y is exact; byte
  *                                                      (32 g + c % 32) * 4 + c / 32 = 127 + e of channel c, group g
  * Key k of a block is in group k / 32 (its 32-key half).
- * With the second plane, V = (hi + lo / 16) * 2^e to about 7 significant bits instead of 4.
+ * With the residual plane, V = (hi + lo) * 2^e to about 7 significant bits instead of 4 (|y - hi| <= 16 fits bf6
+ * unscaled). A residual row holds the 32 codes of each 32-key half as 24 bytes (code k of the half at bits
+ * 6k .. 6k + 5): half 0's bytes 0-15, half 1's bytes 0-15, then the halves' bytes 16-23, half 1's first in
+ * channels whose bit 4 is set. A NaN or an infinity in V gives hi a NaN code and lo a code of magnitude 28.
  * Position p of a 64-key V block holds key 32*((p&31)>>4) + 8*((p>>2)&3) + 4*(p>>5) + (p&3).
  *
  * Quantised Q (per call): q8 int8 [BH][Lp][128], q_scale fp32 [BH][Lp/32], Lp = Lq rounded up to 256;
@@ -204,7 +208,8 @@ int lbw_quant_mx_fp8(const void* x, int x_is_fp32, int64_t rows, int64_t rows_pa
  * in a chunk (the token window of lingbot/layers/kv_cache.py:23-81). Writes bf16
  * out [batch][lq][heads][128] with strides o_s_batch, o_s_tok, o_s_head. S = q8 . k8 in int32 on the
  * int8 MFMA, online softmax in the exp2 domain, P in e4m3 on the fp8 MFMA with V's E8M0 block scales applied by
- * the MFMA itself (a second fp8 product with the residual plane, scaled 2^-4 lower, when v8lo is not null), fp32
+ * the MFMA itself (when v8lo is not null, a second product of the residual plane with bf6(P / 16) on the 6-bit
+ * MFMA, at twice the fp8 rate, scaled back by 2^4), fp32
  * accumulation, 1 / row sum applied at the end (the row sum adds the e4m3 P the products apply, formed on the
  * matrix core; the reference sums the unrounded P). Replaces the fused Sage kernel call (lingbot/layers/sage_preq.py:
  * 126-127; experiments/modules/sage_kvq.py:107-110). seg_slot / seg_len are host arrays. `workspace` holds

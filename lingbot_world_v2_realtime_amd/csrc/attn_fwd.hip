@@ -1,5 +1,6 @@
 // Quantized attention forward for gfx950: int8 QK^T on v_mfma_i32_32x32x32_i8, online softmax in the exp2
-// domain, e4m3 P times e4m3 V on v_mfma_f32_32x32x64_f8f6f4, fp32 accumulation.
+// domain, e4m3 P times e4m3 V on v_mfma_scale_f32_32x32x64_f8f6f4 and, for V's optional residual plane, bf6(P / 16)
+// times the bf6 residual on the same instruction with both operands 6-bit (twice the fp8 rate), fp32 accumulation.
 //
 // Tile: 8 waves x 32 queries = 256 queries of one batch*head. Each wave computes S^T = K Q^T (keys on the MFMA
 // M axis, queries on N), so a lane holds one query and 16 keys of each 32x32 S tile: the row max is in-lane
@@ -60,7 +61,7 @@ __device__ __forceinline__ XcdPlan xcd_plan(const AttnArgs& a, int x) {
 
 constexpr int S_MASKED = (int)0xFF800000;      // bits of -inf: the int max ignores it, exp2 gives 0
 constexpr int E8M0_ONE = 0x7F7F7F7F;           // MFMA block scale 1.0 in every byte
-constexpr int E8M0_LO = 0x7B7B7B7B;            // 2^-4: the lo plane carries (y - hi) * 16
+constexpr int E8M0_P16 = 0x83838383;           // 2^4: the residual product's P operand is bf6(P / 16)
 
 // max of a value over the two lane halves (lanes l and l ^ 32 hold the same query)
 __device__ __forceinline__ int halves_max_i(int x) {
@@ -103,18 +104,23 @@ struct Piece {      // online-softmax state of one wave after a range of key blo
 // (one wave of each per SIMD) and run the same per-block program with a phase offset of one barrier: while one
 // group issues its MFMAs (S = K Q^T of block j, then P V of block j - 1) the other computes the softmax of its
 // block, so the matrix cores and the vector ALUs work at the same time. In its MFMA phase every wave streams
-// one 1 KB piece of each tile of block j + LEAD into LDS with direct global -> LDS loads, through NSTAGE stages;
+// one piece of each tile of block j + LEAD into LDS with direct global -> LDS loads, through NSTAGE stages;
 // group A waits for its pieces at the end of a softmax phase, group B at the end of an MFMA phase (in the fast
 // form of the pass both groups wait at both points), so each block has landed before the barrier that opens its
-// first MFMA phase. Stage layout (24 KB; the block's scales go to records of their own, below):
-// K tile 64 rows x 128 B, V tile 128 channels x 64 B, V residual tile; 16-byte chunks XOR-swizzled by row
-// (K: chunk ^ ((row >> 1) & 7), V: chunk ^ ((row >> 2) & 3)) so that the fragment reads of the MFMA operands hit
-// 16 distinct bank groups per 16 lanes, and every 1 KB of a tile is one contiguous DMA of 64 lanes x 16 B.
+// first MFMA phase. Stage layout (22 KB; the block's scales go to records of their own, below):
+// K tile 64 rows x 128 B, V tile 128 channels x 64 B, V residual tile 128 channels x 48 B (bf6 codes, the row layout
+// of the re-quant). K and V 16-byte chunks are XOR-swizzled by row (K: chunk ^ ((row >> 1) & 7), V: chunk ^
+// ((row >> 2) & 3)) so that the fragment reads of the MFMA operands hit 16 distinct bank groups per 16 lanes, and
+// every 1 KB of those tiles is one contiguous DMA of 64 lanes x 16 B. The residual rows need no swizzle: at their
+// 48-byte stride the 16-byte reads of 16 consecutive channels cover the 64 banks once, and their 8-byte tails,
+// stored swapped in channels with bit 4 set, do the same for 32 channels; each wave moves 768 B (48 lanes x 16 B).
 constexpr int AT_WAVES = 8;
 constexpr int AT_THREADS = 64 * AT_WAVES;
 constexpr int NSTAGE = 6;
 constexpr int LEAD = 4;                        // NSTAGE - LEAD >= 2: a stage is free one phase before its reload
-constexpr int ST_K = 0, ST_V = 8192, ST_VLO = 16384, ST_BYTES = 24576;
+constexpr int ST_K = 0, ST_V = 8192, ST_VLO = 16384, ST_BYTES = ST_VLO + V_LO_TILE;
+constexpr int VLO_PIECE = V_LO_TILE / AT_WAVES;   // 768 B of the residual tile per wave
+static_assert(ST_BYTES % 1024 == 0 && VLO_PIECE == 48 * 16, "stage layout");
 static_assert(QT == 32 * AT_WAVES, "query tile");
 // Scales of the block in each stage ([stage][wave w][36 B]): wave w's record holds dwords 8 w .. 8 w + 7 of the
 // block's V scale table, then the block's K scale (each wave its own copy). Table dword l is the E8M0 block scales
@@ -174,28 +180,31 @@ __device__ __forceinline__ v16i mfma_i8_from_magic(v4i a, v4i b) {
   return d;
 }
 
-// A block's loads in one asm, M0 saved once and restored once around them: the K, V and (with TWO) V-residual tiles,
-// 16 bytes per lane, each a wave-uniform base plus a 32-bit per-lane byte offset (the global instruction's
-// scalar-base form: no 64-bit address per lane to form); then the wave's scale record by lanes 0-8 from 64-bit
-// per-lane addresses (`sp`: lanes 0-7 this wave's 32 bytes of the V scale table, lane 8 the K scale), lane i
-// writing M0 + 4 i (EXEC narrowed around that load and restored before the asm ends, so no branch).
+// A block's loads in one asm, M0 saved once and restored once around them: the K and V tiles, 16 bytes per lane,
+// and (with TWO) the V-residual tile, 16 bytes per lane of lanes 0-47 (EXEC narrowed), each a wave-uniform base plus
+// a 32-bit per-lane byte offset (the global instruction's scalar-base form: no 64-bit address per lane to form);
+// then the wave's scale record by lanes 0-8 from 64-bit per-lane addresses (`sp`: lanes 0-7 this wave's 32 bytes of
+// the V scale table, lane 8 the K scale), lane i writing M0 + 4 i. EXEC is restored before the asm ends, so no
+// branch.
 template <bool TWO>
 __device__ __forceinline__ void dma_block(const void* kb, uint32_t koff, const void* vb, const void* vlb, uint32_t voff,
-                                          uint64_t sp, uint8_t* lk, uint8_t* lv, uint8_t* lvl, uint8_t* lsc) {
+                                          uint32_t vloff, uint64_t sp, uint8_t* lk, uint8_t* lv, uint8_t* lvl,
+                                          uint8_t* lsc) {
   uint32_t keep;
   uint64_t ex;
   if (TWO)
     asm volatile("s_mov_b32 %0, m0\n\t"
                  "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %2, %3\n\t"
                  "s_mov_b32 m0, %7\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %5\n\t"
-                 "s_mov_b32 m0, %9\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %8\n\t"
-                 "s_mov_b64 %1, exec\n\ts_mov_b64 exec, 0x1ff\n\t"
+                 "s_mov_b64 %1, exec\n\ts_mov_b32 exec_hi, 0xffff\n\t"
+                 "s_mov_b32 m0, %9\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %12, %8\n\t"
+                 "s_mov_b64 exec, 0x1ff\n\t"
                  "s_mov_b32 m0, %11\n\ts_nop 0\n\tglobal_load_lds_dword %10, off\n\t"
                  "s_mov_b64 exec, %1\n\t"
                  "s_mov_b32 m0, %0"
                  : "=&s"(keep), "=&s"(ex)
                  : "v"(koff), "s"(kb), "v"(voff), "s"(vb), "s"(lds_addr(lk)), "s"(lds_addr(lv)), "s"(vlb),
-                   "s"(lds_addr(lvl)), "v"(sp), "s"(lds_addr(lsc))
+                   "s"(lds_addr(lvl)), "v"(sp), "s"(lds_addr(lsc)), "v"(vloff)
                  : "memory");
   else
     asm volatile("s_mov_b32 %0, m0\n\t"
@@ -211,13 +220,17 @@ __device__ __forceinline__ void dma_block(const void* kb, uint32_t koff, const v
                  : "memory");
 }
 
-// PV MFMA f of a block: O^T tile f & 3 += V^T fragment (hi plane for f < 4, the residual plane after) times P^T,
-// with V's E8M0 block scales from byte f & 3 of vsc (the byte select is an immediate of the instruction) and P
-// unscaled, or scaled by 2^-4 for the residual plane (a constant operand, so no per-block arithmetic on vsc).
+// PV MFMA f of a block: O^T tile f & 3 += V^T fragment times P^T, with V's E8M0 block scales from byte f & 3 of vsc
+// (the byte select is an immediate of the instruction). f < 4: the e4m3 hi plane times the e4m3 P, unscaled.
+// f >= 4: the residual plane, bf6 x bf6 (both operands 6-bit, so the product runs at twice the fp8 rate: 6 of the
+// 8 operand registers are read), times bf6(P / 16) with the B scale 2^4 (a constant operand, so no per-block
+// arithmetic on vsc).
 template <int F>
-__device__ __forceinline__ void pv_mfma(v16f (&o)[4], const v8i& vf, const v8i& pb, int vsc) {
-  o[F & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, o[F & 3], 0, 0, F & 3, vsc, 0,
-                                                             F < 4 ? E8M0_ONE : E8M0_LO);
+__device__ __forceinline__ void pv_mfma(v16f (&o)[4], const v8i& vf, const v8i& pb, const v8i& pb6, int vsc) {
+  if constexpr (F < 4)
+    o[F & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb, o[F & 3], 0, 0, F & 3, vsc, 0, E8M0_ONE);
+  else
+    o[F & 3] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pb6, o[F & 3], 3, 3, F & 3, vsc, 0, E8M0_P16);
 }
 
 // Key blocks [j0, j1) of one tile for this wave's 32 queries (first query q0). TWO: V has a residual plane.
@@ -252,18 +265,27 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   const v8i ones = rowsum_ones(lane);
   const bool multi = a.n_seg > 1;
 
-  // fragment read offsets in a stage (K: chunk 4g + kk of row 32 mt + lq; V: chunks 2g, 2g + 1 of row 32 mt + lq)
-  int kro[4], vro[2];
+  // fragment read offsets in a stage (K: chunk 4g + kk of row 32 mt + lq; V: chunks 2g, 2g + 1 of row 32 mt + lq;
+  // V residual: half g's 16-byte piece and its 8-byte tail in row 32 mt + lq). The tails of odd mt have a base
+  // register of their own: the fragments mt, mt + 1 are read together, and two 8-byte reads from one base would be
+  // merged into one two-address read, whose 4-register result then takes moves to form each fragment's 6
+  // contiguous operand registers.
+  int kro[4], vro[2], lro[3];
   {
     const int s1 = (lq >> 1) & 7, s2 = (lq >> 2) & 3;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) kro[kk] = lq * 128 + (((4 * g + kk) ^ s1) << 4);
 #pragma unroll
     for (int h = 0; h < 2; ++h) vro[h] = ST_V + lq * 64 + (((2 * g + h) ^ s2) << 4);
+    lro[0] = ST_VLO + lq * V_LO_ROW + 16 * g;
+    lro[1] = ST_VLO + lq * V_LO_ROW + 32 + 8 * (g ^ ((lq >> 4) & 1));
+    lro[2] = lro[1] + 32 * V_LO_ROW;
+    asm volatile("" : "+v"(lro[2]));   // opaque: not folded back into lro[1] + offset
   }
 
-  // loader: wave w moves 1 KB piece w of each 8 KB tile (K, V and the V residual)
+  // loader: wave w moves 1 KB piece w of each 8 KB tile (K, V) and 768 B piece w of the 6 KB V residual tile
   int koff, voff;
+  const int vloff = VLO_PIECE * w + 16 * lane;   // lanes 0-47 load
   {
     const int kr = 8 * w + (lane >> 3), vr = 16 * w + (lane >> 2);
     koff = kr * 128 + (((lane & 7) ^ ((kr >> 1) & 7)) << 4);
@@ -287,15 +309,16 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     const int64_t blk = (int64_t)bb + a.seg_fb[cc];
     kbase = k8 + (sbh * a.cap + blk * KB) * D;
     vbase = v8 + (sbh * a.nbc + blk) * TILE_BYTES;
-    if (TWO) vlbase = v8lo + (sbh * a.nbc + blk) * TILE_BYTES;
+    if (TWO) vlbase = v8lo + (sbh * a.nbc + blk) * V_LO_TILE;
     sptr = lane < 8 ? (uint64_t)(uintptr_t)(v_scale + (sbh * a.nbc + blk) * 256 + w * 32 + 4 * lane)
                     : (uint64_t)(uintptr_t)(k_scale + sbh * a.nbc + blk);
   };
   seek(lc, lb);
   auto issue = [&](int stage) {
-    uint8_t* sb = lds + stage * ST_BYTES + w * 1024;
-    dma_block<TWO>(kbase, (uint32_t)koff, vbase, TWO ? (const void*)vlbase : nullptr, (uint32_t)voff, sptr,
-                   sb + ST_K, sb + ST_V, sb + ST_VLO, lds + TAB_SC + stage * SC_STAGE + w * SC_WAVE);
+    uint8_t* sb = lds + stage * ST_BYTES;
+    dma_block<TWO>(kbase, (uint32_t)koff, vbase, TWO ? (const void*)vlbase : nullptr, (uint32_t)voff,
+                   (uint32_t)vloff, sptr, sb + ST_K + w * 1024, sb + ST_V + w * 1024, sb + ST_VLO + w * VLO_PIECE,
+                   lds + TAB_SC + stage * SC_STAGE + w * SC_WAVE);
   };
   auto advance = [&](auto fast) {   // fast: the next block is in the same chunk (lrem >= 2)
     if (!decltype(fast)::value && --lrem == 0) {   // the fast form's steps are taken off lrem after the run
@@ -307,7 +330,7 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     } else {
       kbase += TILE_BYTES;
       vbase += TILE_BYTES;
-      if (TWO) vlbase += TILE_BYTES;
+      if (TWO) vlbase += V_LO_TILE;
       sptr += sstep;
     }
   };
@@ -357,7 +380,8 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
   phase_barrier();
   if (!grp_a) phase_barrier();   // group B runs one phase behind
 
-  v8i pb = {0, 0, 0, 0, 0, 0, 0, 0};
+  v8i pb = {0, 0, 0, 0, 0, 0, 0, 0};    // P^T as e4m3 bytes
+  v8i pb6 = {0, 0, 0, 0, 0, 0, 0, 0};   // the same keys as bf6(P / 16) codes (TWO; registers 6 and 7 unused)
   int stage = 0, pstage = 0;
   int it = 0;
   // One pass: the MFMA phase of block it and the softmax phase of block it. The fast form assumes what holds for
@@ -377,7 +401,14 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     const uint8_t* sv = lds + pstage * ST_BYTES;
     constexpr int NVF = TWO ? 8 : 4;   // V fragments (one per PV MFMA): hi plane mt 0..3, then lo plane mt 0..3
     auto vfrag = [&](int f) {
-      const int off = (f >= 4 ? ST_VLO - ST_V : 0) + (f & 3) * 2048;
+      if (f >= 4) {   // 32 bf6 codes: 16 + 8 bytes (operand registers 6 and 7 are not read)
+        const int off = (f & 3) * 32 * V_LO_ROW;
+        const v4i a = *(const v4i*)(sv + lro[0] + off);
+        const v2i b = *(const v2i*)(sv + ((f & 1) ? lro[2] + (off - 32 * V_LO_ROW) : lro[1] + off));
+        const v8i r = {a[0], a[1], a[2], a[3], b[0], b[1], 0, 0};
+        return r;
+      }
+      const int off = (f & 3) * 2048;
       const v4i lo = *(const v4i*)(sv + vro[0] + off);
       const v4i hi = *(const v4i*)(sv + vro[1] + off);
       const v8i r = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -388,14 +419,14 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
     int vsc;
     auto pv = [&](int f, const v8i& vf) {   // f is a constant once the loop below is unrolled
       switch (f) {
-        case 0: pv_mfma<0>(st.o, vf, pb, vsc); break;
-        case 1: pv_mfma<1>(st.o, vf, pb, vsc); break;
-        case 2: pv_mfma<2>(st.o, vf, pb, vsc); break;
-        case 3: pv_mfma<3>(st.o, vf, pb, vsc); break;
-        case 4: pv_mfma<4>(st.o, vf, pb, vsc); break;
-        case 5: pv_mfma<5>(st.o, vf, pb, vsc); break;
-        case 6: pv_mfma<6>(st.o, vf, pb, vsc); break;
-        default: pv_mfma<7>(st.o, vf, pb, vsc); break;
+        case 0: pv_mfma<0>(st.o, vf, pb, pb6, vsc); break;
+        case 1: pv_mfma<1>(st.o, vf, pb, pb6, vsc); break;
+        case 2: pv_mfma<2>(st.o, vf, pb, pb6, vsc); break;
+        case 3: pv_mfma<3>(st.o, vf, pb, pb6, vsc); break;
+        case 4: pv_mfma<4>(st.o, vf, pb, pb6, vsc); break;
+        case 5: pv_mfma<5>(st.o, vf, pb, pb6, vsc); break;
+        case 6: pv_mfma<6>(st.o, vf, pb, pb6, vsc); break;
+        default: pv_mfma<7>(st.o, vf, pb, pb6, vsc); break;
       }
     };
     // Both halves run on every pass, so the LDS waits need no control-flow joins: at it == n the QK MFMAs read
@@ -533,16 +564,35 @@ __device__ __forceinline__ void attend_range(const AttnArgs& a, const int8_t* __
       tk = beta - m_ref + (P_OFFSET - RESCALE_SLACK);
     }
     const float kc = tk - S_MAGIC_F * cb;
-    float p[32];
+    // p_i = exp2(S_i * cb + kc), i = 0..31, held as pe[k] = p_2k and po[k] = p_2k+1: the operand order of the bf6
+    // conversion below, so neither packing needs a register move.
+    v16f pe, po;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(si[i]), cb, kc));
-    // P^T B operand: byte 16 mt' + 4 i + j of this lane = p[16 mt' + 4 i + j] (keys 32 mt' + 8 i + 4 g + j).
+    for (int k2 = 0; k2 < 16; ++k2) {
+      pe[k2] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(si[2 * k2]), cb, kc));
+      po[k2] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(si[2 * k2 + 1]), cb, kc));
+    }
+    // P^T B operand: byte 16 mt' + 4 i + j of this lane = p_(16 mt' + 4 i + j) (keys 32 mt' + 8 i + 4 g + j).
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
       // both halves of the word are written, so the previous word serves as the "old" operand (no zeroing move)
-      int wd = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * r], p[4 * r + 1], pb[r], false);
-      wd = __builtin_amdgcn_cvt_pk_fp8_f32(p[4 * r + 2], p[4 * r + 3], wd, true);
+      int wd = __builtin_amdgcn_cvt_pk_fp8_f32(pe[2 * r], po[2 * r], pb[r], false);
+      wd = __builtin_amdgcn_cvt_pk_fp8_f32(pe[2 * r + 1], po[2 * r + 1], wd, true);
       pb[r] = wd;
+    }
+    if constexpr (TWO) {
+      // The residual product's operand, bf6(p / 16): code c of this lane is first the key of byte c of pb. A lane
+      // of the 6-bit operand holds one whole K-block (lane half g: K-block g, the keys of V scale group g), where an
+      // fp8 lane holds 16 values of each: so the lower half's codes 16-31 (dwords 3-5) and the upper half's codes
+      // 0-15 (dwords 0-2) trade places across the halves. Lane half g then holds positions 16 g .. 16 g + 15 and
+      // 32 + 16 g .. 47 + 16 g, in the code order of the residual plane's rows.
+      const v6i c6 = cvt_bf6_x32(pe, po, P_LO_SCALE);
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+        const auto sw = __builtin_amdgcn_permlane32_swap((unsigned)c6[r], (unsigned)c6[r + 3], false, false);
+        pb6[r] = (int)sw[0];
+        pb6[r + 3] = (int)sw[1];
+      }
     }
     // next block of the compute cursor
     if (!FAST && --crem == 0 && c + 1 < a.n_seg) {   // the fast form's steps are taken off crem after the run

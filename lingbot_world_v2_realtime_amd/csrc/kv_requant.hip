@@ -6,8 +6,10 @@
 //                   (key group, channel): group g is the block's 32-token half g, the K-block g of the attention's
 //                   64-deep fp8 PV MFMA, whose per-lane E8M0 block scale then applies the scale. 2^e takes the
 //                   group's amax into (224, 448]; y = V * 2^-e (exact) -> e4m3
-//                   hi = rn(y) and, when a second plane is given, lo = rn((y - hi) * 16), both in the permuted block
-//                   layout, and the block's 256-byte E8M0 table (byte (32 g + c % 32) * 4 + c / 32 = 127 + e of
+//                   hi = rn(y) and, when a second plane is given, the bf6 (e3m2) residual lo = rn(y - hi) over the
+//                   same positions (|y - hi| <= 16 fits bf6 unscaled), packed 48 bytes per channel row (the two
+//                   scale groups' 24 bytes as 16 + 16 + 8 + 8, the 8-byte tails swapped in channels with bit 4
+//                   set), and the block's 256-byte E8M0 table (byte (32 g + c % 32) * 4 + c / 32 = 127 + e of
 //                   channel c, group g: the attention lane that scales channel c's row for group g reads dword
 //                   32 g + c % 32 and selects byte c / 32).
 //   2. kv_finalize: per (batch*head, layer, 16 channels), the half-block sums added into blocks and 4-block
@@ -39,7 +41,9 @@ constexpr int FIN_U = 8;       // super-block sums per lane the finaliser holds 
 // its e4m3 bytes of one channel are 4 adjacent positions (one dword) of the permuted layout. Steps separated by
 // workgroup barriers.
 struct VBlockLds {
-  uint32_t tile[2][D * 16];   // hi / lo planes: [channel][16 dwords], dword xor-swizzled by channel >> 3
+  // [channel][16 dwords], dword xor-swizzled by channel >> 3: the hi plane's 4 e4m3 bytes of a position quad, and
+  // the residual plane's 4 bf6 codes of it in the low 24 bits
+  uint32_t tile[2][D * 16];
   float gmax[4][D];           // per wave: max |V| of each channel over the wave's 16 keys
   float rec[2][D];            // 2^-e of [group][channel]
   uint32_t table[64];         // the block's E8M0 scale table, stored out as 64 dwords
@@ -82,7 +86,7 @@ __device__ __forceinline__ void vblock_scale(VBlockLds& s) {
   ((uint8_t*)s.table)[t] = (uint8_t)(127 + e);
 }
 
-// Step 3: e4m3 bytes into the transposed LDS tile.
+// Step 3: e4m3 bytes into the transposed LDS tile, and with `two` the residual plane's bf6 codes beside them.
 __device__ __forceinline__ void vblock_quant(const float (&vf)[4][8], bool two, VBlockLds& s) {
   const int t = threadIdx.x, cg = t & 15, kq = t >> 4;
   float rec[8];
@@ -92,27 +96,22 @@ __device__ __forceinline__ void vblock_quant(const float (&vf)[4][8], bool two, 
     rec[0] = r0.x; rec[1] = r0.y; rec[2] = r0.z; rec[3] = r0.w;
     rec[4] = r1.x; rec[5] = r1.y; rec[6] = r1.z; rec[7] = r1.w;
   }
-  uint32_t vb[8], vl[8];   // per channel: 4 e4m3 bytes (hi, lo) of keys 4kq .. 4kq+3
+  uint32_t vb[8];   // per channel: 4 e4m3 bytes of keys 4kq .. 4kq+3
+  float y[4][8];
+  int pk[4][4];     // e4m3 bytes of (key j, channels 2 i, 2 i + 1)
 #pragma unroll
-  for (int c = 0; c < 8; ++c) { vb[c] = 0; vl[c] = 0; }
+  for (int c = 0; c < 8; ++c) vb[c] = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int c = 0; c < 8; c += 2) {
       // |V| * 2^-e <= 448 by the choice of e, and the product is exact (a power-of-two factor), so no clamp: a NaN
       // or an infinity becomes an e4m3 NaN (as the reference's per-channel quantiser makes its channel NaN)
-      const float y0 = __fmul_rn(vf[j][c], rec[c]);
-      const float y1 = __fmul_rn(vf[j][c + 1], rec[c + 1]);
-      const int pk = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-      vb[c] |= ((uint32_t)pk & 0xFFu) << (8 * j);
-      vb[c + 1] |= (((uint32_t)pk >> 8) & 0xFFu) << (8 * j);
-      if (two) {   // residual plane: (y - hi) * 16 is exact in fp32 and within the e4m3 range
-        const float r0 = __fmul_rn(__fsub_rn(y0, __builtin_amdgcn_cvt_f32_fp8(pk, 0)), V_LO_SCALE);
-        const float r1 = __fmul_rn(__fsub_rn(y1, __builtin_amdgcn_cvt_f32_fp8(pk, 1)), V_LO_SCALE);
-        const uint32_t pl = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false);
-        vl[c] |= (pl & 0xFFu) << (8 * j);
-        vl[c + 1] |= ((pl >> 8) & 0xFFu) << (8 * j);
-      }
+      y[j][c] = __fmul_rn(vf[j][c], rec[c]);
+      y[j][c + 1] = __fmul_rn(vf[j][c + 1], rec[c + 1]);
+      pk[j][c >> 1] = __builtin_amdgcn_cvt_pk_fp8_f32(y[j][c], y[j][c + 1], 0, false);
+      vb[c] |= ((uint32_t)pk[j][c >> 1] & 0xFFu) << (8 * j);
+      vb[c + 1] |= (((uint32_t)pk[j][c >> 1] >> 8) & 0xFFu) << (8 * j);
     }
   // row = channel, dword = position / 4
   const int pdw = v_pos_of_key(kq * 4) >> 2;
@@ -120,27 +119,65 @@ __device__ __forceinline__ void vblock_quant(const float (&vf)[4][8], bool two, 
   for (int c = 0; c < 8; ++c) {
     const int ch = cg * 8 + c;
     s.tile[0][ch * 16 + (pdw ^ (ch >> 3))] = vb[c];
-    if (two) s.tile[1][ch * 16 + (pdw ^ (ch >> 3))] = vl[c];
+  }
+  if (two) {
+    // Residual plane: y - hi is exact in fp32 and |y - hi| <= 16 lies inside bf6's range. One conversion of the
+    // 32 residuals, sources ordered so that code 4 c + j is the residual of (channel c, key j): channel c's 4
+    // codes are then bits 24 c .. 24 c + 23 of the result, the packed form of its 4 adjacent positions.
+    v16f s0, s1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)   // channels 2 i (byte 0 of the e4m3 pairs) and 2 i + 1 (byte 1)
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        s0[4 * i + m] = __fsub_rn(y[2 * m][2 * i], __builtin_amdgcn_cvt_f32_fp8(pk[2 * m][i], 0));
+        s1[4 * i + m] = __fsub_rn(y[2 * m + 1][2 * i], __builtin_amdgcn_cvt_f32_fp8(pk[2 * m + 1][i], 0));
+        s0[4 * i + 2 + m] = __fsub_rn(y[2 * m][2 * i + 1], __builtin_amdgcn_cvt_f32_fp8(pk[2 * m][i], 1));
+        s1[4 * i + 2 + m] = __fsub_rn(y[2 * m + 1][2 * i + 1], __builtin_amdgcn_cvt_f32_fp8(pk[2 * m + 1][i], 1));
+      }
+    const v6i r = cvt_bf6_x32(s0, s1, 1.f);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int bit = 24 * c, dw = bit >> 5, sh = bit & 31;
+      const uint32_t w0 = (uint32_t)r[dw], w1 = sh > 8 ? (uint32_t)r[dw + 1] : 0u;
+      const uint32_t vl = (sh > 8 ? __builtin_amdgcn_alignbit(w1, w0, sh) : w0 >> sh) & 0xFFFFFFu;
+      const int ch = cg * 8 + c;
+      s.tile[1][ch * 16 + (pdw ^ (ch >> 3))] = vl;
+    }
   }
 }
 
-// Step 4: the tiles out, each store instruction 1 KB contiguous per wave: store s of thread t writes bytes
-// 4096 s + 16 t .. + 15 of a plane's 8 KB tile (channel 64 s + t / 4, dwords 4 (t % 4) .. + 3 of its row); threads
-// 0-63 also write the scale table, a dword each.
+// Step 4: the tiles out. hi plane: each store instruction 1 KB contiguous per wave, store s of thread t writing
+// bytes 4096 s + 16 t .. + 15 of the 8 KB tile (channel 64 s + t / 4, dwords 4 (t % 4) .. + 3 of its row). Residual
+// plane: thread t packs the 24 bytes of channel t / 2, scale group g = t % 2 (8 position quads of 3 bytes: positions
+// 16 g .. 16 g + 15, then 32 + 16 g .. 47 + 16 g, the 32 codes one lane of the 6-bit PV operand holds, since such a
+// lane holds a whole K-block) and writes their first 16 at 16 g of the 48-byte row and the last 8 at 32 + 8 g, or
+// 40 - 8 g in channels with bit 4 set; a wave writes 1.5 KB of contiguous rows. Threads 0-63 also write the scale
+// table, a dword each.
 __device__ __forceinline__ void vblock_store(const VBlockLds& s, uint8_t* __restrict__ v8, uint8_t* __restrict__ v8lo,
                                              uint8_t* __restrict__ v_scale, int64_t tile) {
   const int t = threadIdx.x, dw = 4 * (t & 3);
   if (t < 64) ((uint32_t*)(v_scale + tile * 256))[t] = s.table[t];
-  for (int pl = 0; pl < (v8lo ? 2 : 1); ++pl) {
-    uint8_t* vout = (pl ? v8lo : v8) + tile * (D * KB) + 16 * t;
+  {
+    uint8_t* vout = v8 + tile * (D * KB) + 16 * t;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       const int ch = 64 * half + (t >> 2);
       uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) w[i] = s.tile[pl][ch * 16 + ((dw + i) ^ (ch >> 3))];
+      for (int i = 0; i < 4; ++i) w[i] = s.tile[0][ch * 16 + ((dw + i) ^ (ch >> 3))];
       store_once(vout + 4096 * half, v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]});
     }
+  }
+  if (v8lo) {
+    const int ch = t >> 1, g = t & 1;
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = s.tile[1][ch * 16 + ((4 * g + i + (i & 4)) ^ (ch >> 3))];   // quads of group g
+    uint8_t* row = v8lo + tile * V_LO_TILE + ch * V_LO_ROW;
+    store_once(row + 16 * g, v4i{(int)(w[0] | (w[1] << 24)), (int)((w[1] >> 8) | (w[2] << 16)),
+                                 (int)((w[2] >> 16) | (w[3] << 8)), (int)(w[4] | (w[5] << 24))});
+    store_once(row + 32 + 8 * (g ^ ((ch >> 4) & 1)), v2i{(int)((w[5] >> 8) | (w[6] << 16)),
+                                                         (int)((w[6] >> 16) | (w[7] << 8))});
   }
 }
 

@@ -20,7 +20,11 @@ constexpr int KB = 64;            // keys per K scale block / V block
 constexpr int QG = 32;            // query rows per Q scale
 constexpr int QT = 256;           // Lq is padded to whole tiles of this many rows (the attention tile)
 constexpr float V_MAX = 448.f;
-constexpr float V_LO_SCALE = 16.f;           // second e4m3 V plane: the residual of the first, times 16
+// The optional second V plane holds the residual y - e4m3(y) of y = V / 2^e as bf6 (OCP e3m2) codes, 32 of a
+// 32-key half in 24 bytes, rows of 48 bytes per channel and block; the attention multiplies it by bf6(P / P_LO_SCALE).
+constexpr int V_LO_ROW = 48;
+constexpr int V_LO_TILE = D * V_LO_ROW;      // 6 KB: the residual plane of one 64-key block
+constexpr float P_LO_SCALE = 16.f;
 constexpr float AMAX_FLOOR = 1e-7f;
 constexpr float P_OFFSET = 8.807f;           // log2(448): P = exp2(s - m + P_OFFSET) <= 448
 // A row's reference max m moves only when a block's max exceeds it by more than RESCALE_SLACK (log2 units);
@@ -43,6 +47,17 @@ __device__ __forceinline__ void store_once(void* p, v2i v) { __builtin_nontempor
 __device__ __forceinline__ void store_once(void* p, v4i v) { __builtin_nontemporal_store(v, (v4i*)p); }
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// 32 floats -> 32 bf6 codes (192 bits, code k at bits 6 k .. 6 k + 5): code 2 k is a[k] / scale and code 2 k + 1 is
+// b[k] / scale, rounded to nearest even, magnitudes above 28 saturating (a NaN gives 28 with its sign). Inline asm
+// with an early-clobber result: the builtin's result register range was allowed to overlap its sources, which the
+// instruction does not support (it overwrote sources it had yet to read).
+typedef int v6i __attribute__((ext_vector_type(6)));
+__device__ __forceinline__ v6i cvt_bf6_x32(const v16f& a, const v16f& b, float scale) {
+  v6i r;
+  asm("v_cvt_scalef32_2xpk16_bf6_f32 %0, %1, %2, %3" : "=&v"(r) : "v"(a), "v"(b), "v"(scale));
+  return r;
+}
 
 // fp32 -> nearest bf16 (ties to even) as fp32; finite inputs.
 __device__ __forceinline__ float bf16_round(float x) {

@@ -12,6 +12,7 @@ Q_TILE = 256
 Q_GROUP = 32
 MAX_SEGMENTS = 8
 V_TABLE_BYTES = 256   # E8M0 V scales per 64-key block: 2 key groups x 128 channels
+V_LO_ROW = 48         # bytes of a channel's 64 bf6 residual codes in a block
 ctypes_i32 = ctypes.c_int32
 
 
@@ -60,9 +61,10 @@ class RingCache:
     """Quantised K/V ring for `layers` layers x `slots` chunk slots of capacity `cap` tokens (a multiple of 64).
 
     Device layout (include/lbw_attn.h): k8 int8 [L, S, BH, cap, 128]; k_scale fp32 [L, S, BH, cap/64];
-    km fp32 [L, S, BH, 128]; v8 (and, with v_terms=2, the residual plane v8lo) uint8 [L, S, BH, cap/64, 128, 64];
-    v_scale uint8 [L, S, BH, cap/64, 256], the E8M0 V scales of each 64-key block (byte (32 g + c % 32) * 4 + c / 32
-    = 127 + e for channel c and key group g, the keys 32 g .. 32 g + 31 of the block).
+    km fp32 [L, S, BH, 128]; v8 uint8 [L, S, BH, cap/64, 128, 64] (e4m3); with v_terms=2 the residual plane v8lo
+    uint8 [L, S, BH, cap/64, 128, 48] (bf6 codes, 48 bytes per channel and block); v_scale uint8
+    [L, S, BH, cap/64, 256], the E8M0 V scales of each 64-key block (byte (32 g + c % 32) * 4 + c / 32 = 127 + e for
+    channel c and key group g, the keys 32 g .. 32 g + 31 of the block).
     """
 
     def __init__(self, layers, batch, heads, cap, slots, device, v_terms=2, zero=True):
@@ -81,7 +83,7 @@ class RingCache:
         self.km = new(layers, slots, bh, HEAD_DIM, dtype=torch.float32, device=dev)
         self.v_terms = v_terms
         self.v8 = new(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev)
-        self.v8lo = new(layers, slots, bh, nb, HEAD_DIM, K_BLOCK, dtype=torch.uint8, device=dev) \
+        self.v8lo = new(layers, slots, bh, nb, HEAD_DIM, V_LO_ROW, dtype=torch.uint8, device=dev) \
             if v_terms == 2 else None
         self.v_scale = torch.empty(layers, slots, bh, nb, V_TABLE_BYTES, dtype=torch.uint8, device=dev)
         if zero:

@@ -18,7 +18,8 @@ quantisers and its documentation of the fused kernel:
   the group's amax into (224, 448], the top binade of e4m3: V / 2^e is exact, e4m3's relative precision is the
   same in every binade, and a power-of-two scale rides on the fp8 MFMA's E8M0 block-scale operand (per A row and
   32-key block) instead of a multiply of the accumulator. A group's scale needs only its own block, so a chunk's
-  V is quantised in one pass over it.
+  V is quantised in one pass over it. A second plane carries the residual y - hi of y = V / 2^e as bf6 (OCP
+  e3m2) codes, which the attention multiplies by bf6(P / 16) on the 6-bit MFMA (at twice the fp8 rate).
 - Logits: S = q8 . k8 in int32 (experiments/bench_attn/h2_tiles/README.md:45), dequantised with
   q_scale * k_scale * sm_scale * log2(e) into the exp2 domain; P = exp2(s - m + 8.807) <= 448 cast to e4m3
   (experiments/bench_attn/phi_calib.md:11-16); O = sum P V / sum P, with the V scale
@@ -57,8 +58,9 @@ HEAD_DIM = 128
 V_MAX = 448.0           # e4m3 max; the V scale maps amax to it
 AMAX_FLOOR = 1e-7
 P_OFFSET = 8.807        # log2(448): P = exp2(s - m + P_OFFSET) <= 448
-V_TERMS = 2             # e4m3 V terms: hi, and lo = the residual * 16
-V_LO_SCALE = 16.0
+V_TERMS = 2             # V terms: hi = e4m3(y), and the residual plane lo = bf6(y - hi)
+P_LO_SCALE = 16.0       # the residual product takes P as bf6(P / 16); the MFMA's B scale 2^4 restores the factor
+V_LO_ROW = 48           # bytes of one channel's 64 bf6 residual codes in a block
 RESCALE_SLACK = 2.0     # tau: a row's reference max moves only when a block max exceeds it by more than tau
 LOG2E = 1.4426950408889634
 
@@ -103,6 +105,66 @@ def e4m3_encode_nonfinite(x):
 def e4m3_decode(bits):
     """e4m3fn bits (uint8) -> fp32."""
     return bits.view(torch.float8_e4m3fn).to(torch.float32)
+
+
+def bf6_encode(x):
+    """fp32 tensor -> bf6 codes (OCP e3m2: sign in bit 5, exponent bits 4:2 with bias 3, mantissa bits 1:0, no inf
+    or NaN codes) as uint8 0..63, rounded to nearest even the way gfx950's v_cvt_scalef32_2xpk16_bf6_f32 converts:
+    magnitudes above 28 and infinities saturate to 28, a NaN becomes 28 with the NaN's sign bit, and a value that
+    rounds to zero keeps its sign. The step is 2^(e - 2) in the binade [2^e, 2^(e + 1)), e = -2 .. 4, and 2^-4
+    below 0.25 (the subnormals)."""
+    a = x.abs().to(torch.float32)
+    a = torch.where(torch.isnan(a), torch.full_like(a, 32.0), a.clamp_max(32.0))   # 32 saturates below
+    _, ex = torch.frexp(a)                                          # a in [2^(ex - 1), 2^ex)
+    eb = torch.where(a < 0.25, torch.full_like(ex, -2), ex - 1).clamp_max(4)
+    q = torch.round(torch.ldexp(a, 2 - eb))                         # 4..8 in a normal binade, 0..4 below
+    mag = (4 * (eb + 2) + q.to(torch.int32)).clamp_max(31)          # q = 8 carries into the next binade
+    return (mag | (torch.signbit(x).to(torch.int32) << 5)).to(torch.uint8)
+
+
+def bf6_decode(bits):
+    """bf6 (e3m2) codes (uint8 0..63) -> fp32."""
+    b = bits.to(torch.int32)
+    e, m = (b >> 2) & 7, (b & 3).to(torch.float32)
+    mag = torch.where(e > 0, (4.0 + m) * torch.ldexp(torch.ones_like(m), e - 5), m / 16.0)
+    return torch.where((b >> 5) & 1 == 1, -mag, mag)
+
+
+BF6_POS_OF_CODE = np.array([16 * g + c + (c & 16) for g in range(2) for c in range(32)])   # [group g][code c]
+
+
+def pack_bf6_rows(codes):
+    """bf6 codes [..., C, 64 positions] (C channels) -> packed rows uint8 [..., C, 48]. Group g holds the positions
+    of V scale group g (16 g .. 16 g + 15 and 32 + 16 g .. 47 + 16 g, the keys 32 g .. 32 g + 31): its code c is
+    position 16 g + c + (c & 16), because a lane of the 6-bit MFMA operand holds one whole K-block (lane half g:
+    K-block g), where an fp8 lane holds 16 values of each. A group's 32 codes are 24 bytes, code c at bits
+    6 c .. 6 c + 5 little endian; a row is group 0's bytes 0-15, group 1's bytes 0-15, then the two 8-byte tails
+    (bytes 16-23 of each group): group 0's first in channels whose bit 4 is clear, group 1's first where it is set.
+    A lane reads its group's 24 bytes as one 16-byte and one 8-byte LDS load; at the 48-byte row stride the 16-byte
+    loads of 16 consecutive channels cover the 64 banks once, and with the tails swapped so do the 8-byte loads
+    of 32."""
+    c = codes.to(torch.int64)[..., torch.from_numpy(BF6_POS_OF_CODE)].reshape(*codes.shape[:-1], 2, 8, 4)
+    w = c[..., 0] | (c[..., 1] << 6) | (c[..., 2] << 12) | (c[..., 3] << 18)      # 4 codes = 3 bytes
+    b = torch.stack([w & 255, (w >> 8) & 255, (w >> 16) & 255], dim=-1).reshape(*codes.shape[:-1], 2, 24)
+    swap = (((torch.arange(codes.shape[-2]) >> 4) & 1) == 1)[:, None]
+    t0 = torch.where(swap, b[..., 1, 16:], b[..., 0, 16:])
+    t1 = torch.where(swap, b[..., 0, 16:], b[..., 1, 16:])
+    return torch.cat([b[..., 0, :16], b[..., 1, :16], t0, t1], dim=-1).to(torch.uint8)
+
+
+def unpack_bf6_rows(rows):
+    """Inverse of pack_bf6_rows: uint8 [..., C, 48] -> codes [..., C, 64]."""
+    r = rows.to(torch.int64)
+    swap = (((torch.arange(rows.shape[-2]) >> 4) & 1) == 1)[:, None]
+    t0 = torch.where(swap, r[..., 40:48], r[..., 32:40])
+    t1 = torch.where(swap, r[..., 32:40], r[..., 40:48])
+    halves = torch.stack([torch.cat([r[..., 0:16], t0], -1), torch.cat([r[..., 16:32], t1], -1)], -2)
+    b = halves.reshape(*rows.shape[:-1], 2, 8, 3)
+    w = b[..., 0] | (b[..., 1] << 8) | (b[..., 2] << 16)
+    c = torch.stack([(w >> (6 * i)) & 63 for i in range(4)], dim=-1).reshape(*rows.shape[:-1], 64)
+    out = torch.empty_like(c)
+    out[..., torch.from_numpy(BF6_POS_OF_CODE)] = c
+    return out.to(torch.uint8)
 
 
 def _as_lhd(x):
@@ -210,15 +272,19 @@ def v_exponents_of_table(table):
 
 
 def quant_v(v):
-    """v bf16 / fp16 [L, H, D] -> (v8, v8lo uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, the E8M0
-    scale table uint8 [H, nb, 256] of v_scale_table).
+    """v bf16 / fp16 [L, H, D] -> (v8 uint8 e4m3 bits [H, nb, D, 64] in the permuted key order, v8lo the residual
+    plane uint8 [H, nb, D, 48] of bf6 codes over the same positions (pack_bf6_rows), the E8M0 scale table uint8
+    [H, nb, 256] of v_scale_table).
 
     Scales are powers of two, one per (64-key block, key group, channel): group g of a block holds its keys
-    32 g .. 32 g + 31, the 32-deep K-block g of the 64-deep fp8 PV MFMA (bytes 16 g .. 16 g + 15 of every lane's
-    operand, which the permuted layout fills with those keys), whose E8M0 block scale of the A operand applies per
-    row and K-block -- so the MFMA applies the scale itself. Two e4m3
-    terms: y = v / 2^e (exact, |y| <= 448); hi = e4m3(y); lo = e4m3((y - hi) * 16), so v ~ (hi + lo / 16) * 2^e.
-    y - hi is exact in fp32 (hi is y rounded to 3 mantissa bits) and |y - hi| * 16 <= 256 stays in range."""
+    32 g .. 32 g + 31, the 32-deep K-block g of the 64-deep PV MFMA (bytes 16 g .. 16 g + 15 of every lane's fp8
+    operand, which the permuted layout fills with those keys; all 32 codes of lane half g's 6-bit operand, which
+    pack_bf6_rows fills with them), whose E8M0 block scale of the A operand applies per row and K-block -- so the
+    MFMA applies the scale itself. Two terms:
+    y = v / 2^e (exact, |y| <= 448); hi = e4m3(y); lo = bf6(y - hi), so v ~ (hi + lo) * 2^e. y - hi is exact in
+    fp32 (hi is y rounded to 3 mantissa bits) and |y - hi| <= 16 (half an e4m3 step below 448) lies inside bf6's
+    range, so lo needs no scale of its own. A NaN or an infinity in V gives hi a NaN code and lo the code of 28
+    (bf6 has no NaN; the sign is the NaN residual's)."""
     v = _as_lhd(v)
     n, h, d = v.shape
     lp = pad_to(n, K_BLOCK)
@@ -229,12 +295,12 @@ def quant_v(v):
     y[:, :n] = v.float().permute(1, 0, 2)
     y = y * recip                                   # |y| <= 448 for finite V: no clamp, a NaN or inf stays one
     hi = e4m3_encode_nonfinite(y)
-    lo = e4m3_encode_nonfinite((y - e4m3_decode(hi)) * V_LO_SCALE)
+    lo = bf6_encode(y - e4m3_decode(hi))
     planes = []
     for bits in (hi, lo):
         bits = bits.view(h, lp // K_BLOCK, K_BLOCK, d)[:, :, torch.from_numpy(V_KEY_OF_POS)]   # [h, b, pos, d]
         planes.append(bits.permute(0, 1, 3, 2).contiguous())
-    return planes[0], planes[1], v_scale_table(e)
+    return planes[0], pack_bf6_rows(planes[1]), v_scale_table(e)
 
 
 def requant(k, v):
@@ -255,21 +321,32 @@ def span(chunk):
     return first, n, b0, pad_to(first + n, K_BLOCK) // K_BLOCK - b0
 
 
-def dequant_v(chunk, terms=None):
-    """e4m3 V of a quantised chunk back to fp32 [H, first + n, D] in key order (slot keys 0 .. first + n - 1), in
-    true units: (hi + lo / 16) * 2^e with each key's group scale (or hi alone with terms=1, the default for a
-    chunk whose "v8lo" is None)."""
-    if terms is None:   # a chunk quantised without the residual plane has one term
-        terms = V_TERMS if chunk.get("v8lo") is not None else 1
+def dequant_v_planes(chunk):
+    """The V planes of a quantised chunk in true units, fp32 [H, first + n, D] each in key order (slot keys
+    0 .. first + n - 1): (hi * 2^e, lo * 2^e) with each key's group scale; lo is None for a chunk whose "v8lo" is
+    None (quantised without the residual plane)."""
     h, nb, d, _ = chunk["v8"].shape
     end = chunk.get("first", 0) + chunk["n"]
     e = v_exponents_of_table(chunk["v_scale"])[:, :, torch.from_numpy(V_GROUP_OF_KEY)]   # [h, nb, key, d]
     scale = torch.ldexp(torch.ones(e.shape), e)
-    out = 0
-    for bits, w in ((chunk["v8"], 1.0), (chunk["v8lo"], 1.0 / V_LO_SCALE))[:terms]:
-        vals = e4m3_decode(bits)[:, :, :, torch.from_numpy(V_POS_OF_KEY)]   # [h, nb, d, key]
-        out = out + vals.permute(0, 1, 3, 2) * w
-    return (out * scale).reshape(h, nb * K_BLOCK, d)[:, :end]
+    pos = torch.from_numpy(V_POS_OF_KEY)
+    out = []
+    for vals in (e4m3_decode(chunk["v8"]),
+                 bf6_decode(unpack_bf6_rows(chunk["v8lo"])) if chunk.get("v8lo") is not None else None):
+        if vals is not None:   # [h, nb, d, position] -> [h, keys, d]
+            vals = (vals[:, :, :, pos].permute(0, 1, 3, 2) * scale).reshape(h, nb * K_BLOCK, d)[:, :end]
+        out.append(vals)
+    return out[0], out[1]
+
+
+def dequant_v(chunk, terms=None):
+    """V of a quantised chunk back to fp32 [H, first + n, D] in key order (slot keys 0 .. first + n - 1), in true
+    units: (hi + lo) * 2^e with each key's group scale (or hi alone with terms=1, the default for a chunk whose
+    "v8lo" is None)."""
+    hi, lo = dequant_v_planes(chunk)
+    if terms is None:
+        terms = V_TERMS if lo is not None else 1
+    return hi + lo if terms == 2 else hi
 
 
 def qk_logits(q8, k8):
@@ -319,9 +396,11 @@ def attn_schedule(n_tiles, nb, gx):
 def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=None, p_round=True):
     """Online softmax over tile-relative key blocks [j0, j1) (numbered across the chunks in order) for the
     query rows `qf` (q8 as fp32) -> (o in true V units, m, l). The reference max m of a row moves only when a
-    block's max exceeds it by more than `tau`. The row sum l adds up the P that the PV product multiplies: the e4m3
-    P (so O / l normalises exactly the weights applied to V), or with p_round=False the unrounded fp32 P. The
-    reference's Sage kernel sums the unrounded P instead (a deviation of ~2^-5 / sqrt(keys) relative in l)."""
+    block's max exceeds it by more than `tau`. The row sum l adds up the P that the hi plane's PV product
+    multiplies: the e4m3 P (so O / l normalises exactly the weights applied to hi), or with p_round=False the
+    unrounded fp32 P. The residual plane's product takes P as bf6(P / 16) * 16, whose rounding (2^-3 relative)
+    acts on a term at most 2^-4 of V. The reference's Sage kernel sums the unrounded P instead (a deviation of
+    ~2^-5 / sqrt(keys) relative in l)."""
     rows, d = qf.shape[0], qf.shape[1]
     m_run = torch.full((rows,), float("-inf"))
     l_run = torch.zeros(rows)
@@ -352,7 +431,11 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
             pr = e4m3_decode(e4m3_encode(p)) if p_round else p
             l_run = l_run + pr.sum(dim=1)
             # V in true units: its group scales are powers of two, exact, the factors the MFMA's block scale applies
-            o = o + torch.matmul(pr, vdec[ci][hh, k0:k1])
+            hi, lo = vdec[ci]
+            o = o + torch.matmul(pr, hi[hh, k0:k1])
+            if lo is not None:
+                pl = bf6_decode(bf6_encode(p / P_LO_SCALE)) * P_LO_SCALE if p_round else p
+                o = o + torch.matmul(pl, lo[hh, k0:k1])
         j += nbc
     return o, m_run, l_run
 
@@ -363,12 +446,13 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
     slot's 64-key blocks in sequence (keys outside the read range masked), a reference row max m, and per block
       b = max_j S_ij * cb + beta,  m_new = b if b > m + tau else m,  alpha = exp2(m - m_new),
       o = alpha * o,  l = alpha * l,  P_ij = exp2(S_ij * cb + beta - m_new + 8.807 - tau)  (<= 448),
-      l += sum P,  o += e4m3(P) . (V8 * 2^e)  (V in true units, its group scales applied),
+      l += sum e4m3(P),  o += e4m3(P) . (hi * 2^e) + bf6(P / 16) * 16 . (lo * 2^e)  (V in true units, its
+      group scales applied),
     with cb = q_scale * k_scale * sm_scale * log2(e) and beta = q . mean_k of the chunk (several chunks only);
     finally out = o / l. Each block's contribution is in true V units, so a chunk switch needs no rescale.
     With `schedule_gx` (the kernel's workgroups per XCD), tiles the kernel splits between workgroups are
     computed piece by piece from a fresh state and merged by `merge_partials`.
-    p_round=False skips the e4m3 rounding of P (a checking mode: the result is then exact softmax attention of
+    p_round=False skips the rounding of P (a checking mode: the result is then exact softmax attention of
     the dequantised logits and V, whatever the block order, running max or split).
     Returns fp32 [Lq, H, D].
     """
@@ -378,7 +462,7 @@ def attention(q, chunks, sm_scale=None, q_block=1024, schedule_gx=None, tau=None
     sl2 = _sl2(sm_scale, d)
     q8, qs = quant_q(q)
     multi = len(chunks) > 1
-    vdec = [dequant_v(c) for c in chunks]
+    vdec = [dequant_v_planes(c) for c in chunks]
     bias = [q_bias(q, c["km"]) * sl2 if multi else None for c in chunks]
     nb = sum(span(c)[3] for c in chunks)
     q_tiles = pad_to(lq, Q_TILE) // Q_TILE
@@ -426,7 +510,7 @@ def attention_exact_max(q, chunks, sm_scale=None, q_block=1024):
     sl2 = _sl2(sm_scale, d)
     q8, qs = quant_q(q)
     multi = len(chunks) > 1
-    vdec = [dequant_v(c) for c in chunks]
+    vdec = [dequant_v_planes(c) for c in chunks]
     bias = [q_bias(q, c["km"]) * sl2 if multi else None for c in chunks]
     out = torch.empty(lq, h, d, dtype=torch.float32)
     for hh in range(h):
@@ -449,7 +533,11 @@ def attention_exact_max(q, chunks, sm_scale=None, q_block=1024):
                 p = torch.exp2(logits[ci] - m[:, None] + P_OFFSET)
                 den = den + p.sum(dim=1)
                 p8 = e4m3_decode(e4m3_encode(p))
-                num = num + torch.matmul(p8, vdec[ci][hh, c.get("first", 0):])
+                hi, lo = vdec[ci]
+                num = num + torch.matmul(p8, hi[hh, c.get("first", 0):])
+                if lo is not None:
+                    pl = bf6_decode(bf6_encode(p / P_LO_SCALE)) * P_LO_SCALE
+                    num = num + torch.matmul(pl, lo[hh, c.get("first", 0):])
             out[a:e, hh] = num / den[:, None]
     return out
 

@@ -52,6 +52,15 @@ def _nan_equal(a, b):
     return torch.equal(na, nb) and torch.equal(a[~na], b[~nb])
 
 
+def _residual_equal(got, want, hi):
+    """bf6 residual rows: the same codes, except where hi is a NaN code; there the residual is a NaN, which bf6 has
+    no code for, and both sides hold 28 with a sign that is not defined (the sign of NaN - NaN)."""
+    g, w = emu.unpack_bf6_rows(got), emu.unpack_bf6_rows(want)
+    nan = (hi & 0x7F) == 0x7F
+    return (torch.equal(g[~nan], w[~nan]) and bool(((g[nan] & 0x1F) == 0x1F).all())
+            and bool(((w[nan] & 0x1F) == 0x1F).all()))
+
+
 def test_requant_nonfinite_v():
     """A NaN or an infinity in V: the same scale table as the oracle (a NaN does not enter its half-block's amax,
     an infinity takes it to exponent 120), NaN codes where they are, the other codes bit-exact; the attention is
@@ -69,7 +78,8 @@ def test_requant_nonfinite_v():
     ref = emu.requant(k, v)
     nb = (n + 63) // 64
     assert torch.equal(ring.v_scale[0, 0, :, :nb].cpu(), ref["v_scale"])
-    assert _nan_equal(ring.v8[0, 0, :, :nb].cpu(), ref["v8"]) and _nan_equal(ring.v8lo[0, 0, :, :nb].cpu(), ref["v8lo"])
+    assert _nan_equal(ring.v8[0, 0, :, :nb].cpu(), ref["v8"])
+    assert _residual_equal(ring.v8lo[0, 0, :, :nb].cpu(), ref["v8lo"], ref["v8"])
     assert torch.equal(ring.k8[0, 0, :, :nb * 64].cpu(), ref["k8"])
     # the attention over a V with the NaN only
     v[0, 70, 1, 9] = 1.0
@@ -296,9 +306,13 @@ def test_attention_row_sum_of_rounded_p():
     h, n, lq = 3, 1000, 300
     q = torch.randn(1, lq, h, 128).to(torch.bfloat16)
     k = (torch.randn(1, n, h, 128) * 2).to(torch.bfloat16)
-    v = torch.randn(1, 1, h, 128).expand(1, n, h, 128).to(torch.bfloat16).contiguous()
+    # row values with 3 mantissa bits: exact in e4m3 once scaled, so the residual plane is zero and only the hi
+    # product (whose P the row sum adds) contributes
+    v = emu.e4m3_decode(emu.e4m3_encode(torch.randn(1, 1, h, 128)))
+    v = v.expand(1, n, h, 128).to(torch.bfloat16).contiguous()
     out = _attn_gpu(q, k, v)[0]
     vrow = emu.dequant_v(emu.requant(k, v))[:, 0]                       # [h, 128], fp32
+    assert torch.equal(vrow, v[0, 0].float())
     want = vrow.to(torch.bfloat16).float()[None].expand(lq, -1, -1)
     same = (out == want).float().mean().item()
     print(f"bf16-identical share {same:.5f}, max rel {((out - want).abs() / want.abs()).max():.3e}")

@@ -15,7 +15,7 @@ def test_ring_layout_sizes():
     assert r.k8.shape == (3, 4, 10, 192, 128) and r.k8.dtype == torch.int8
     assert r.k_scale.shape == (3, 4, 10, 3)
     assert r.km.shape == (3, 4, 10, 128)
-    assert r.v8.shape == r.v8lo.shape == (3, 4, 10, 3, 128, 64)
+    assert r.v8.shape == (3, 4, 10, 3, 128, 64) and r.v8lo.shape == (3, 4, 10, 3, 128, 48)
     assert r.v_scale.shape == (3, 4, 10, 3, 256) and r.v_scale.dtype == torch.uint8
     assert kernels.RingCache(1, 1, 1, 64, 2, "cpu", v_terms=1).v8lo is None
     with pytest.raises(ValueError):

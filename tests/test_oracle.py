@@ -46,6 +46,45 @@ def test_e4m3_encoder_matches_format_definition():
     assert got == want
 
 
+def bf6_ref(x):
+    """Nearest bf6 (OCP e3m2, bias 3, no inf / NaN) code of a Python float by enumerating the 64 codes: ties to the
+    even mantissa, magnitudes beyond 28 saturating, a value that rounds to zero keeping its sign."""
+    if math.isnan(x):
+        return 0x1F | (0x20 if math.copysign(1.0, x) < 0 else 0)
+    best, a = None, min(abs(x), 28.0)                   # 28 is the largest magnitude
+    for code in range(32):
+        e, m = (code >> 2) & 7, code & 3
+        mag = (m / 4.0) * 2.0 ** -2 if e == 0 else (1 + m / 4.0) * 2.0 ** (e - 3)
+        key = (abs(mag - a), m & 1)
+        if best is None or key < best[0]:
+            best = (key, code)
+    return best[1] | (0x20 if math.copysign(1.0, x) < 0 else 0)
+
+
+def test_bf6_encoder_matches_format_definition():
+    """bf6_encode against the enumeration above over every value, every midpoint (the ties), values past the
+    range and random ones; and against the codes gfx950's v_cvt_scalef32_2xpk16_bf6_f32 gave for special inputs
+    (scale 1): NaN and infinities saturate to 28 with their sign, 26 ties to 24, 0.03125 to +0."""
+    vals = sorted({float(emu.bf6_decode(torch.tensor([c], dtype=torch.uint8))) for c in range(64)})
+    xs = vals + [(a + b) / 2 for a, b in zip(vals, vals[1:])] + [30.0, -31.99, 1e30, 0.03124, 0.03126, -1e-40]
+    xs += list(np.random.default_rng(9).uniform(-30, 30, 400)) + list(np.random.default_rng(10).uniform(-0.3, 0.3, 200))
+    x32 = torch.tensor(xs, dtype=torch.float32)
+    assert emu.bf6_encode(x32).tolist() == [bf6_ref(float(v)) for v in x32.tolist()]
+    codes = torch.arange(64, dtype=torch.uint8)
+    assert torch.equal(emu.bf6_encode(emu.bf6_decode(codes)), codes)
+    special = torch.tensor([float("nan"), float("inf"), -float("inf"), 28.0, 32.0, -0.0, 0.03125, 0.09375, 26.0,
+                            18.0, 7.5, 3.75, 0.21875, -16.0])
+    special[0] = -special[0]                              # a negative NaN
+    assert emu.bf6_encode(special).tolist() == [0x3F, 0x1F, 0x3F, 0x1F, 0x1F, 0x20, 0x00, 0x02, 0x1E, 0x1C, 0x18,
+                                                 0x14, 0x04, 0x3C]
+
+
+def test_bf6_rows_pack_and_unpack():
+    codes = torch.randint(0, 64, (2, 3, 128, 64), dtype=torch.uint8, generator=torch.Generator().manual_seed(8))
+    rows = emu.pack_bf6_rows(codes)
+    assert rows.shape == (2, 3, 128, 48) and torch.equal(emu.unpack_bf6_rows(rows), codes)
+
+
 # ---------------------------------------------------------------- int8 quantisers
 
 def test_int8_group_quant_closed_form():
@@ -219,7 +258,9 @@ def test_v_nonfinite_values():
     assert bool(nan[0, 0, 3, pos]) and int(nan.sum()) == 2 and bool(nan[1, 1, 9, int(emu.V_POS_OF_KEY[6])])
     keep = torch.ones_like(nan)
     keep[1, 1, 9] = False                              # the infinite value's block and channel
+    alo, clo = emu.unpack_bf6_rows(alo), emu.unpack_bf6_rows(clo)
     assert torch.equal(a8[keep & ~nan], c8[keep & ~nan]) and torch.equal(alo[keep & ~nan], clo[keep & ~nan])
+    assert bool(((alo[nan] & 0x1F) == 0x1F).all())    # bf6 has no NaN code: the NaN residual saturates to 28
     e = emu.v_exponents_of_table(at)
     assert int(e[1, 1, 0, 9]) == 120 and int(emu.v_exponents_of_table(ct)[1, 1, 0, 9]) != 120
     grp0 = torch.tensor([int(emu.V_POS_OF_KEY[k]) for k in range(32)])   # the infinity's half: keys 0-31
@@ -243,7 +284,7 @@ def test_v_quant_layout_and_two_term_bound():
     n, h = 130, 2
     v = (torch.randn(n, h, 128) * torch.rand(1, h, 128) * 4).to(torch.bfloat16)
     v8, v8lo, table = emu.quant_v(v)
-    assert v8.shape == (h, 3, 128, 64) and table.shape == (h, 3, 256)
+    assert v8.shape == (h, 3, 128, 64) and v8lo.shape == (h, 3, 128, 48) and table.shape == (h, 3, 256)
     # each key's scale, from the group amax computed here directly (keys 32 g .. 32 g + 31 of block b)
     vp = torch.zeros(192, h, 128)
     vp[:n] = v.float()
@@ -264,10 +305,28 @@ def test_v_quant_layout_and_two_term_bound():
     # one e4m3 term: half an e4m3 step (2^-4 relative, 2^-10 absolute in the subnormal range)
     tol1 = torch.maximum(y.abs() * 2.0 ** -4, torch.full_like(y, 2.0 ** -10))
     assert torch.all((one - y).abs() <= tol1)
-    # two terms: the residual (at most half a step of hi) carried to e4m3 precision again
-    tol2 = torch.maximum(y.abs() * 2.0 ** -8, torch.full_like(y, 2.0 ** -13))
+    # two terms: the residual r = y - hi (|r| <= half a step of hi, 2^-4 |y|) carried to bf6 precision: half a bf6
+    # step, 2^-3 |r| <= 2^-7 |y| for |r| >= 0.25, and 2^-5 absolute below (bf6's subnormal step is 2^-4)
+    tol2 = torch.maximum(y.abs() * 2.0 ** -7, torch.full_like(y, 2.0 ** -5))
     assert torch.all((two - y).abs() <= tol2)
     assert (two - y).abs().mean() < (one - y).abs().mean() / 8
+    # the residual row layout, read bit by bit: channel c, position p of V scale group g = (p >> 4) & 1 is code
+    # k = (p & 15) + 16 (p >> 5) of the group, at bits 6 k .. 6 k + 5 of its 24 bytes: bytes 0-15 at 16 g of the row,
+    # bytes 16-23 at 32 + 8 g (32 + 8 (1 - g) when c & 16)
+    hi = emu.e4m3_decode(v8)
+    for hh, b, c in ((0, 0, 3), (1, 2, 17), (0, 1, 126), (1, 1, 48)):
+        row = [int(x) for x in v8lo[hh, b, c]]
+        for p in range(64):
+            half, k = (p >> 4) & 1, (p & 15) + 16 * (p >> 5)
+            assert int(emu.V_KEY_OF_POS[p]) // 32 == half        # the group of the position is its key's half
+            tail = 32 + 8 * (half ^ ((c >> 4) & 1))
+            data = row[16 * half:16 * half + 16] + row[tail:tail + 8]
+            word = int.from_bytes(bytes(data), "little")
+            code = (word >> (6 * k)) & 63
+            key = 64 * b + int(emu.V_KEY_OF_POS[p])
+            if key < n:
+                r = float(y[hh, key, c]) - float(hi[hh, b, c, p])
+                assert code == int(emu.bf6_encode(torch.tensor([r]))[0]), (hh, b, c, p)
 
 
 # ---------------------------------------------------------------- logits
@@ -418,22 +477,25 @@ def test_online_split_and_chunk_switch_exact_without_p_rounding(gx):
 
 
 def test_row_sum_adds_the_rounded_p():
-    """O / l must normalise exactly the weights the PV product applies. With V the same in every key row (each
-    channel its own value, so every half-block quantises it to the same codes) the output is that row whatever
-    the logits, to fp32 rounding, across chunks, a chunk switch and split tiles. A row sum of the unrounded P
-    would scale the output by sum(e4m3(P)) / sum(P), about 1e-3 away from 1 for such weights, which the bound
-    sees."""
+    """O / l must normalise exactly the weights the hi plane's PV product applies. With V the same in every key
+    row (each channel its own value, so every half-block quantises it to the same codes) the output is that row
+    whatever the logits, to fp32 rounding, across chunks, a chunk switch and split tiles. The row's values have
+    3 mantissa bits, so the scaled y is exact in e4m3 and the residual plane is zero (its product takes P rounded
+    to bf6, which the row sum does not normalise exactly). A row sum of the unrounded P would scale the output by
+    sum(e4m3(P)) / sum(P), about 1e-3 away from 1 for such weights, which the bound sees."""
     g = torch.Generator().manual_seed(41)
     h, lq = 2, 300
     q = torch.randn(1, lq, h, 128, generator=g).to(torch.bfloat16)
-    row = torch.randn(1, 1, h, 128, generator=g)
+    row = emu.e4m3_decode(emu.e4m3_encode(torch.randn(1, 1, h, 128, generator=g)))
     chunks = []
     for i, n in enumerate((200, 333)):
         k = (torch.randn(1, n, h, 128, generator=g) * (1 + i)).to(torch.bfloat16)
         chunks.append(emu.requant(k, row.expand(1, n, h, 128).to(torch.bfloat16).contiguous()))
     vrow = emu.dequant_v(chunks[0])[:, 0]
+    assert torch.equal(vrow, row[0, 0])
     for c in chunks:
         assert torch.equal(emu.dequant_v(c)[:, :c["n"]], vrow[:, None].expand(-1, c["n"], -1))
+        assert not emu.unpack_bf6_rows(c["v8lo"]).bitwise_and(0x1F).any()   # the residual plane is all zero
     for gx in (None, 16):
         got = emu.attention(q, chunks, schedule_gx=gx)
         assert ((got - vrow[None]).abs() <= 1e-5 * vrow.abs()[None] + 1e-7).all()
