@@ -79,13 +79,13 @@ def requant_bytes(n, h=H, d=D, v_planes=1):
 
 def requant_moved_bytes(n, h=H, d=D):
     """Bytes the re-quant's three passes move per layer, as built: bf16 K read twice (statistics, then the
-    quantiser: its mean is a reduction over the whole chunk) and V once; int8 K, both e4m3 V planes and the scale
-    table of every 64-token block written; the K scales and mean; the fp32 K column sums of each 32-token
-    half-block written and read back by the finaliser. 86.2 MB per layer at 6032 tokens x 12 heads, the 2.59 GB
-    per 30 layers that FETCH_SIZE / WRITE_SIZE count (profiles/hbm_traffic_per_call.md)."""
+    quantiser: its mean is a reduction over the whole chunk) and V once; int8 K, the e4m3 V plane, its bf6 residual
+    plane (0.75 byte a value) and the scale table of every 64-token block written; the K scales and mean; the fp32 K column sums of each 32-token
+    half-block written and read back by the finaliser. 83.9 MB per layer at 6032 tokens x 12 heads, 2.52 GB per 30
+    layers, 1.1 % below what FETCH_SIZE / WRITE_SIZE count (profiles/hbm_traffic_per_call.md)."""
     nb = (n + 63) // 64
     kv = n * h * d * 2
-    return (2 * kv + kv + nb * 64 * h * d + 2 * nb * 64 * h * d + nb * h * 256 + nb * h * 4 + h * d * 4 +
+    return (2 * kv + kv + 2 * nb * 64 * h * d + nb * 64 * h * d * 3 // 4 + nb * h * 256 + nb * h * 4 + h * d * 4 +
             2 * nb * 2 * h * d * 4)
 
 

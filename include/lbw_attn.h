@@ -30,9 +30,10 @@
  *                                                      (32 g + c % 32) * 4 + c / 32 = 127 + e of channel c, group g
  * Key k of a block is in group k / 32 (its 32-key half).
  * With the residual plane, V = (hi + lo) * 2^e to about 7 significant bits instead of 4 (|y - hi| <= 16 fits bf6
- * unscaled). A residual row holds the 32 codes of each 32-key half as 24 bytes (code k of the half at bits
- * 6k .. 6k + 5): half 0's bytes 0-15, half 1's bytes 0-15, then the halves' bytes 16-23, half 1's first in
- * channels whose bit 4 is set. A NaN or an infinity in V gives hi a NaN code and lo a code of magnitude 28.
+ * unscaled). A residual row holds the 32 codes of each key group g (positions 16g .. 16g + 15, then 32 + 16g ..
+ * 47 + 16g: the keys 32g .. 32g + 31) as 24 bytes (code k of the group at bits 6k .. 6k + 5): group 0's bytes 0-15,
+ * group 1's bytes 0-15, then the groups' bytes 16-23, group 1's first in channels whose bit 4 is set. A NaN or an
+ * infinity in V gives hi a NaN code and lo a code of magnitude 28.
  * Position p of a 64-key V block holds key 32*((p&31)>>4) + 8*((p>>2)&3) + 4*(p>>5) + (p&3).
  *
  * Quantised Q (per call): q8 int8 [BH][Lp][128], q_scale fp32 [BH][Lp/32], Lp = Lq rounded up to 256;
