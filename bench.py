@@ -607,7 +607,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 QK / fp8-e4m3 PV, fp32 accumulate",
+        "dtype": "int8 QK / fp8-e4m3 PV (+ bf6 V residual), fp32 accumulate",
         "data": "synthetic, seeded (Q,V~N(0,1); K~N(0,1)+N(0,3) channel offset; memory ~N(0,1.5))",
         "config": {"workload": "chunk attending to memory: Q [1,6032,12,128] x 24128 keys (current chunk + "
                                "3 cached int8-K/fp8-V chunks); step = current-chunk K/V quant + Q quant + "
