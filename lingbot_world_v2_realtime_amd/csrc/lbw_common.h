@@ -20,8 +20,8 @@ constexpr int KB = 64;            // keys per K scale block / V block
 constexpr int QG = 32;            // query rows per Q scale
 constexpr int QT = 256;           // Lq is padded to whole tiles of this many rows (the attention tile)
 constexpr float V_MAX = 448.f;
-// The optional second V plane holds the residual y - e4m3(y) of y = V / 2^e as bf6 (OCP e3m2) codes, 32 of a
-// 32-key half in 24 bytes, rows of 48 bytes per channel and block; the attention multiplies it by bf6(P / P_LO_SCALE).
+// The optional second V plane holds the residual y - e4m3(y) of y = V / 2^e as bf6 (OCP e3m2) codes, the 32 of a key
+// group in 24 bytes, rows of 48 bytes per channel and block; the attention multiplies it by bf6(P / P_LO_SCALE).
 constexpr int V_LO_ROW = 48;
 constexpr int V_LO_TILE = D * V_LO_ROW;      // 6 KB: the residual plane of one 64-key block
 constexpr float P_LO_SCALE = 16.f;

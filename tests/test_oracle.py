@@ -359,7 +359,7 @@ def test_attention_within_tolerance_of_fp32_softmax():
 def test_attention_invariances():
     q, k, v, _ = emu.make_inputs(128, 320, h=1, seed=7)
     base = emu.attention(q, [emu.requant(k, v)])
-    # V scaled by 2: identical e4m3 planes, doubled scale -> exactly doubled output
+    # V scaled by 2: identical V planes, doubled scale -> exactly doubled output
     v2 = (v.float() * 2).to(torch.bfloat16)
     assert torch.equal(emu.attention(q, [emu.requant(k, v2)]), base * 2)
     # keys shifted by a per-channel constant: with column sums exactly zero on a 1/4 grid the mean is exactly
