@@ -122,6 +122,15 @@ def bf6_encode(x):
     return (mag | (torch.signbit(x).to(torch.int32) << 5)).to(torch.uint8)
 
 
+def bf6_round(x):
+    """bf6_decode(bf6_encode(x)) for finite fp32 x, as values, computed faster: in bf6's normal range (0.25 and up)
+    its rounding is that of e5m2 (the same 2 mantissa bits, to nearest even), saturating at 28; below 0.25 it is
+    the multiple of 2^-4 nearest x (ties to even), which keeps the sign of x."""
+    e5 = x.clamp(-28.0, 28.0).to(torch.float8_e5m2).to(torch.float32).clamp(-28.0, 28.0)
+    sub = torch.round(x * 16.0) / 16.0
+    return torch.where(x.abs() < 0.25, sub, e5)
+
+
 def bf6_decode(bits):
     """bf6 (e3m2) codes (uint8 0..63) -> fp32."""
     b = bits.to(torch.int32)
@@ -434,7 +443,7 @@ def _attend_blocks(qf, qsr, chunks, vdec, beta_of, hh, j0, j1, sl2, tau, stats=N
             hi, lo = vdec[ci]
             o = o + torch.matmul(pr, hi[hh, k0:k1])
             if lo is not None:
-                pl = bf6_decode(bf6_encode(p / P_LO_SCALE)) * P_LO_SCALE if p_round else p
+                pl = bf6_round(p / P_LO_SCALE) * P_LO_SCALE if p_round else p
                 o = o + torch.matmul(pl, lo[hh, k0:k1])
         j += nbc
     return o, m_run, l_run
@@ -536,7 +545,7 @@ def attention_exact_max(q, chunks, sm_scale=None, q_block=1024):
                 hi, lo = vdec[ci]
                 num = num + torch.matmul(p8, hi[hh, c.get("first", 0):])
                 if lo is not None:
-                    pl = bf6_decode(bf6_encode(p / P_LO_SCALE)) * P_LO_SCALE
+                    pl = bf6_round(p / P_LO_SCALE) * P_LO_SCALE
                     num = num + torch.matmul(pl, lo[hh, c.get("first", 0):])
             out[a:e, hh] = num / den[:, None]
     return out

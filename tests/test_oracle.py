@@ -79,6 +79,19 @@ def test_bf6_encoder_matches_format_definition():
                                                  0x14, 0x04, 0x3C]
 
 
+def test_bf6_round_equals_encode_decode():
+    """bf6_round (the attention emulation's fast path) against bf6_decode(bf6_encode(x)): every value, every midpoint
+    and its float neighbours, random values in and past the range, signed zeros."""
+    vals = sorted({float(emu.bf6_decode(torch.tensor([c], dtype=torch.uint8))) for c in range(64)})
+    x = torch.tensor(vals + [(a + b) / 2 for a, b in zip(vals, vals[1:])], dtype=torch.float32)
+    g = torch.Generator().manual_seed(12)
+    x = torch.cat([x, torch.nextafter(x, torch.tensor(100.0)), torch.nextafter(x, torch.tensor(-100.0)),
+                   (torch.rand(50000, generator=g) - 0.2) * 40, torch.rand(20000, generator=g) * 0.5,
+                   torch.tensor([29.0, 30.0, 31.9, 1e9, -0.0, 0.0, -1e-30])])
+    a, b = emu.bf6_round(x), emu.bf6_decode(emu.bf6_encode(x))
+    assert torch.equal(a, b) and torch.equal(torch.signbit(a), torch.signbit(b))
+
+
 def test_bf6_rows_pack_and_unpack():
     codes = torch.randint(0, 64, (2, 3, 128, 64), dtype=torch.uint8, generator=torch.Generator().manual_seed(8))
     rows = emu.pack_bf6_rows(codes)
